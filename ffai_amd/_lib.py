@@ -1,0 +1,109 @@
+"""ctypes binding of include/ffai_attn.h (libffai_attn.so, built in-tree by ffai_amd/build.py).
+
+Loading fails loudly when the library has not been built: there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libffai_attn.so")
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "ffai_attn.h")
+
+FFAI_OK = 0
+FFAI_DECLINED = 1
+FFAI_ERR_INVALID = -1
+FFAI_ERR_HIP = -2
+FFAI_ERR_WORKSPACE = -3
+FFAI_ERR_DEVICE = -4
+
+F32, F16, BF16 = 0, 1, 2
+K_TRANSPOSED, K_ROWS = 0, 1
+ABI_VERSION = 1
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = [
+        ("q_dtype", ctypes.c_int32), ("kv_dtype", ctypes.c_int32), ("out_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32), ("heads_q", ctypes.c_int32), ("heads_kv", ctypes.c_int32),
+        ("q_len", ctypes.c_int32), ("kv_len", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("k_layout", ctypes.c_int32), ("causal", ctypes.c_int32), ("q_offset", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("reserved0", ctypes.c_int32),
+        ("q_strides", ctypes.c_int64 * 4), ("k_strides", ctypes.c_int64 * 4),
+        ("v_strides", ctypes.c_int64 * 4), ("o_strides", ctypes.c_int64 * 4),
+        ("kv_lens", ctypes.c_void_p),
+    ]
+
+
+class TensorView(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("on_device", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * 4), ("strides", ctypes.c_int64 * 4),
+    ]
+
+
+_lib = None
+
+
+class FfaiError(RuntimeError):
+    """An error status (< 0) from the C ABI."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"ffai_attn error {code}: {msg}")
+        self.code = code
+
+
+def header_functions() -> list[str]:
+    """Names of every function include/ffai_attn.h declares."""
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ffai_[a-z0-9_]+)\s*\(", text)))
+
+
+def load():
+    """Load libffai_attn.so (raises if it is missing or built for another ABI)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m ffai_amd.build` "
+                           "(or __graft_entry__.build()); the attention path has no fallback")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    dp = ctypes.POINTER(AttnDesc)
+    tp = ctypes.POINTER(TensorView)
+    L.ffai_attn_abi_version.restype = ctypes.c_int
+    if L.ffai_attn_abi_version() != ABI_VERSION:
+        raise RuntimeError("libffai_attn.so ABI mismatch: rebuild it")
+    L.ffai_attn_desc_init.argtypes = [dp] + [ctypes.c_int32] * 10
+    L.ffai_attn_desc_init.restype = None
+    L.ffai_attn_serves.argtypes = [dp]
+    L.ffai_attn_workspace_bytes.argtypes = [dp, ctypes.POINTER(sz)]
+    L.ffai_attn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
+    L.ffai_serves.argtypes = [tp, tp]
+    L.ffai_attend.argtypes = [tp, tp, tp, ctypes.c_int, tp, vp, sz, vp]
+    L.ffai_attend_workspace_bytes.argtypes = [tp, tp, tp, ctypes.POINTER(sz)]
+    L.ffai_attend_merged.argtypes = [tp, tp, tp, tp, vp]
+    L.ffai_get_decode_min_keys.restype = ctypes.c_int
+    L.ffai_set_decode_min_keys.argtypes = [ctypes.c_int]
+    L.ffai_set_decode_min_keys.restype = None
+    L.ffai_attn_last_error.restype = ctypes.c_char_p
+    for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
+                 "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged"):
+        getattr(L, name).restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return load().ffai_attn_last_error().decode()
+
+
+def check(rc: int) -> int:
+    """Raise FfaiError for error codes; return FFAI_OK / FFAI_DECLINED unchanged."""
+    if rc < 0:
+        raise FfaiError(rc, last_error())
+    return rc

@@ -1,0 +1,390 @@
+// C ABI of the gfx950 fused attention path (include/ffai_attn.h): descriptor validation, the
+// serves predicate, launch planning, and the mirrors of the reference's public functions
+// (crates/ffai-mercury/src/asr/flash_attn.rs: serves :103-129, attend :212-264 with
+// FlashAttnOp::cpu_fwd :266-413, attend_merged :131-158 with MergedAttnOp::cpu_fwd :160-210).
+
+#include "../../include/ffai_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "attn_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+// ---- device check: the kernels are compiled for gfx950 only --------------------------------
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_dev_state[kMaxDevices];  // 0 unknown, 1 gfx950, 2 other
+
+int check_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FFAI_ERR_HIP, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FFAI_ERR_DEVICE, "device index out of range");
+  int st = g_dev_state[dev].load(std::memory_order_acquire);
+  if (st == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+      return fail(FFAI_ERR_HIP, "hipGetDeviceProperties failed");
+    st = (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ? 1 : 2;
+    g_dev_state[dev].store(st, std::memory_order_release);
+  }
+  if (st != 1) return fail(FFAI_ERR_DEVICE, "current device is not gfx950");
+  return FFAI_OK;
+}
+
+// ---- knobs (mirror of knobs::DECODE_MIN_KEYS, knobs.rs:163-168) ------------------------------
+std::atomic<int> g_decode_min_keys{-1};
+
+int decode_min_keys() {
+  int v = g_decode_min_keys.load(std::memory_order_relaxed);
+  if (v < 0) {
+    int init = 8;
+    if (const char* e = std::getenv("FFAI_DECODE_MIN_KEYS")) {
+      char* end = nullptr;
+      const long n = std::strtol(e, &end, 10);
+      if (end != e && *end == '\0' && n >= 0 && n < (1L << 30)) init = (int)n;
+    }
+    int expected = -1;
+    g_decode_min_keys.compare_exchange_strong(expected, init, std::memory_order_relaxed);
+    v = g_decode_min_keys.load(std::memory_order_relaxed);
+  }
+  return v;
+}
+
+constexpr int kMinSeq = 256;  // flash_attn.rs:55 (MIN_SEQ)
+constexpr int kHD = 64;       // flash_attn.rs:50
+
+size_t elem_size(int dt) { return dt == FFAI_F32 ? 4 : 2; }
+bool valid_dtype(int dt) { return dt == FFAI_F32 || dt == FFAI_F16 || dt == FFAI_BF16; }
+
+// ---- descriptor validation ----------------------------------------------------------------
+// Returns FFAI_OK when served, FFAI_DECLINED when well formed but not served,
+// FFAI_ERR_INVALID when malformed. `why` receives the reason.
+int check_desc(const ffai_attn_desc* d, std::string* why) {
+  if (!d) { *why = "null descriptor"; return FFAI_ERR_INVALID; }
+  if (!valid_dtype(d->q_dtype) || !valid_dtype(d->kv_dtype) || !valid_dtype(d->out_dtype)) {
+    *why = "unknown dtype"; return FFAI_ERR_INVALID;
+  }
+  if (d->batch < 1 || d->heads_q < 1 || d->heads_kv < 1 || d->q_len < 1 || d->kv_len < 1) {
+    *why = "sizes must be positive"; return FFAI_ERR_INVALID;
+  }
+  if (d->heads_q % d->heads_kv != 0) { *why = "heads_q must be a multiple of heads_kv"; return FFAI_ERR_INVALID; }
+  if (d->k_layout != FFAI_K_TRANSPOSED && d->k_layout != FFAI_K_ROWS) { *why = "unknown k_layout"; return FFAI_ERR_INVALID; }
+  if (d->causal != 0 && d->causal != 1) { *why = "causal must be 0 or 1"; return FFAI_ERR_INVALID; }
+  if (d->q_offset < 0) { *why = "q_offset must be >= 0"; return FFAI_ERR_INVALID; }
+  if (!(d->scale > 0.f) || !std::isfinite(d->scale)) { *why = "scale must be finite and > 0"; return FFAI_ERR_INVALID; }
+  const int64_t* all[4] = {d->q_strides, d->k_strides, d->v_strides, d->o_strides};
+  for (const int64_t* s : all) {
+    if (s[3] != 1) { *why = "innermost stride must be 1"; return FFAI_ERR_INVALID; }
+    if (s[0] < 0 || s[1] < 0 || s[2] < 1) { *why = "strides must be non-negative (row stride >= 1)"; return FFAI_ERR_INVALID; }
+  }
+  // every index the kernels form must fit in int32 where they use int
+  const int64_t big = (int64_t)1 << 30;
+  if ((int64_t)d->batch * d->heads_q * ((d->q_len + 31) / 32) * ((d->kv_len + 63) / 64) > big) {
+    *why = "problem too large"; return FFAI_ERR_INVALID;
+  }
+  // ---- served combinations
+  if (d->head_dim != 64 && d->head_dim != 128) { *why = "head_dim must be 64 or 128"; return FFAI_DECLINED; }
+  if (d->q_dtype == FFAI_F32) {
+    if (d->out_dtype != FFAI_F32) { *why = "f32 queries produce f32 output"; return FFAI_DECLINED; }
+    if (d->head_dim != 64) { *why = "f32 path serves head_dim 64"; return FFAI_DECLINED; }
+  } else {
+    if (d->kv_dtype != d->q_dtype) { *why = "16-bit queries need K/V of the same type"; return FFAI_DECLINED; }
+    if (d->out_dtype != FFAI_F32 && d->out_dtype != d->q_dtype) {
+      *why = "output must be f32 or the input type"; return FFAI_DECLINED;
+    }
+  }
+  return FFAI_OK;
+}
+
+// Widest aligned access (elements, power of two <= max_vec) valid for every address formed
+// from `base` plus multiples of the three outer strides plus multiples of max_vec.
+int vec_of(const void* base, size_t esize, const int64_t* strides, int max_vec) {
+  int v = max_vec;
+  while (v > 1) {
+    const uintptr_t bytes = (uintptr_t)v * esize;
+    bool ok = ((uintptr_t)base % bytes) == 0;
+    for (int i = 0; i < 3 && ok; ++i) ok = (strides[i] % v) == 0;
+    if (ok) break;
+    v >>= 1;
+  }
+  return v;
+}
+
+struct Plan {
+  int waves;
+  int n_qblk;
+  int n_split;
+  int tiles_per_split;
+  int n_work;
+  size_t ws_bytes;
+};
+
+// Launch shape: 4 waves (128 query rows) per workgroup for long queries, 1 wave (32 rows) for
+// short ones; when that still leaves the 256 CUs short of work, split the keys.
+Plan make_plan(const ffai_attn_desc* d, bool allow_split) {
+  Plan p{};
+  const int64_t bh = (int64_t)d->batch * d->heads_q;
+  const int n_tiles = (d->kv_len + ffai::kBlockN - 1) / ffai::kBlockN;
+  p.waves = d->q_len > 32 ? 4 : 1;
+  int64_t work = bh * ((d->q_len + 32 * p.waves - 1) / (32 * p.waves));
+  if (p.waves == 4 && work < 256) {
+    p.waves = 1;
+    work = bh * ((d->q_len + 31) / 32);
+  }
+  p.n_qblk = (d->q_len + 32 * p.waves - 1) / (32 * p.waves);
+  p.n_split = 1;
+  p.tiles_per_split = n_tiles;
+  if (allow_split && work < 256 && n_tiles >= 2) {
+    const int want = (int)std::min<int64_t>(n_tiles, (512 + work - 1) / work);
+    p.tiles_per_split = (n_tiles + want - 1) / want;
+    p.n_split = (n_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
+  }
+  p.n_work = (int)(work * p.n_split);
+  p.ws_bytes = p.n_split > 1 ? (size_t)bh * p.n_split * d->q_len * (d->head_dim + 2) * 4 : 0;
+  return p;
+}
+
+int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v, void* out,
+            void* ws, size_t ws_bytes, void* stream, bool allow_split) {
+  g_last_error.clear();
+  std::string why;
+  const int rc = check_desc(d, &why);
+  if (rc == FFAI_DECLINED) return fail(FFAI_DECLINED, "declined: " + why);
+  if (rc != FFAI_OK) return fail(rc, why);
+  if (!q || !k || !v || !out) return fail(FFAI_ERR_INVALID, "null operand pointer");
+  const size_t qs = elem_size(d->q_dtype), ks = elem_size(d->kv_dtype), os = elem_size(d->out_dtype);
+  if ((uintptr_t)q % qs || (uintptr_t)k % ks || (uintptr_t)v % ks || (uintptr_t)out % os)
+    return fail(FFAI_ERR_INVALID, "operand pointer not aligned to its element size");
+  const int dev = check_device();
+  if (dev != FFAI_OK) return dev;
+
+  const Plan pl = make_plan(d, allow_split);
+  if (pl.ws_bytes > 0) {
+    if (!ws || ws_bytes < pl.ws_bytes)
+      return fail(FFAI_ERR_WORKSPACE, "workspace smaller than ffai_attn_workspace_bytes");
+    if ((uintptr_t)ws % 16) return fail(FFAI_ERR_INVALID, "workspace must be 16-byte aligned");
+  }
+
+  ffai::FwdParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = out;
+  p.ws = static_cast<float*>(ws);
+  p.kv_lens = d->kv_lens;
+  p.q_sb = d->q_strides[0]; p.q_sh = d->q_strides[1]; p.q_st = d->q_strides[2];
+  p.k_sb = d->k_strides[0]; p.k_sh = d->k_strides[1]; p.k_st = d->k_strides[2];
+  p.v_sb = d->v_strides[0]; p.v_sh = d->v_strides[1]; p.v_st = d->v_strides[2];
+  p.o_sb = d->o_strides[0]; p.o_sh = d->o_strides[1]; p.o_st = d->o_strides[2];
+  p.B = d->batch; p.Hq = d->heads_q; p.Hkv = d->heads_kv; p.Tq = d->q_len; p.Tk = d->kv_len;
+  p.causal = d->causal; p.q_offset = d->q_offset;
+  p.n_qblk = pl.n_qblk; p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split;
+  p.n_work = pl.n_work;
+  const int qmax = d->q_dtype == FFAI_F32 ? 4 : 8;
+  const int kmax = d->q_dtype == FFAI_F32 ? 4 : 8;  // f32 kernel stages K/V four at a time
+  p.q_vec = vec_of(q, qs, d->q_strides, qmax);
+  p.k_vec = vec_of(k, ks, d->k_strides, kmax);
+  p.v_vec = vec_of(v, ks, d->v_strides, kmax);
+  p.o_vec = vec_of(out, os, d->o_strides, 4);
+  p.scale_log2 = d->scale * 1.4426950408889634f;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mode = d->q_dtype == FFAI_F32 ? ffai::kF32 : (d->q_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
+  const int kvt = d->kv_dtype == FFAI_F32 ? ffai::kF32 : (d->kv_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
+  const int ot = d->out_dtype == FFAI_F32 ? ffai::kF32 : (d->out_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
+  hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, d->k_layout == FFAI_K_TRANSPOSED,
+                                  pl.waves, s);
+  if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));
+  if (pl.n_split > 1) {
+    ffai::CombineParams c{};
+    c.ws = p.ws; c.o = out;
+    c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
+    c.B = p.B; c.Hq = p.Hq; c.Tq = p.Tq; c.n_split = p.n_split; c.scale_log2 = p.scale_log2;
+    e = ffai::launch_combine(c, ot, d->head_dim, s);
+    if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("combine launch: ") + hipGetErrorString(e));
+  }
+  return FFAI_OK;
+}
+
+// ---- tensor-view helpers for the mirrors -----------------------------------------------------
+bool contiguous(const ffai_tensor* t) {
+  int64_t expect = 1;
+  for (int i = 3; i >= 0; --i) {
+    if (t->dims[i] != 1 && t->strides[i] != expect) return false;
+    expect *= t->dims[i];
+  }
+  return true;
+}
+
+bool dims_are(const ffai_tensor* t, int64_t a, int64_t b, int64_t c, int64_t d) {
+  return t->dims[0] == a && t->dims[1] == b && t->dims[2] == c && t->dims[3] == d;
+}
+
+void packed_strides(int64_t* s, int64_t d1, int64_t d2, int64_t d3) {
+  s[3] = 1; s[2] = d3; s[1] = d2 * d3; s[0] = d1 * d2 * d3;
+}
+
+// The shape part of attend's accept set (flash_attn.rs:218-262), shared by ffai_attend and
+// ffai_attend_workspace_bytes. Returns FFAI_OK or FFAI_DECLINED.
+int attend_accepts(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v, int masked,
+                   std::string* why) {
+  if (masked) { *why = "masked attention is served by the caller's fallback"; return FFAI_DECLINED; }
+  if (!q->on_device || !kt->on_device || !v->on_device) { *why = "host tensors"; return FFAI_DECLINED; }
+  if (q->dtype != FFAI_F32) { *why = "q must be f32"; return FFAI_DECLINED; }
+  const bool kv_half = kt->dtype == FFAI_F16;
+  if (kv_half && v->dtype != FFAI_F16) { *why = "K f16 needs V f16"; return FFAI_DECLINED; }
+  if (!kv_half && (kt->dtype != FFAI_F32 || v->dtype != FFAI_F32)) { *why = "K/V must be f32 or f16"; return FFAI_DECLINED; }
+  const int64_t b = q->dims[0], heads = q->dims[1], qlen = q->dims[2], hd = q->dims[3];
+  if (b != 1 || hd != kHD) { *why = "batch 1, head_dim 64 only"; return FFAI_DECLINED; }
+  if (kt->dims[0] != 1 || kt->dims[1] != heads || kt->dims[2] != kHD) { *why = "kt shape"; return FFAI_DECLINED; }
+  const int64_t keys = kt->dims[3];
+  if (!dims_are(v, 1, heads, keys, kHD)) { *why = "v shape"; return FFAI_DECLINED; }
+  const int64_t floor = qlen == 1 ? decode_min_keys() : kMinSeq;
+  if (keys < floor) { *why = "fewer keys than the floor"; return FFAI_DECLINED; }
+  if (qlen != 1 && qlen != keys) { *why = "qlen must be 1 or keys"; return FFAI_DECLINED; }
+  return FFAI_OK;
+}
+
+void attend_desc(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
+                 ffai_attn_desc* d) {
+  const int heads = (int)q->dims[1], qlen = (int)q->dims[2], keys = (int)kt->dims[3];
+  ffai_attn_desc_init(d, FFAI_F32, kt->dtype, FFAI_F32, 1, heads, heads, qlen, keys, kHD,
+                      FFAI_K_TRANSPOSED);
+  (void)v;
+}
+
+}  // namespace
+
+extern "C" {
+
+void ffai_attn_desc_init(ffai_attn_desc* d, int32_t q_dtype, int32_t kv_dtype, int32_t out_dtype,
+                         int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t q_len,
+                         int32_t kv_len, int32_t head_dim, int32_t k_layout) {
+  if (!d) return;
+  std::memset(d, 0, sizeof(*d));
+  d->q_dtype = q_dtype; d->kv_dtype = kv_dtype; d->out_dtype = out_dtype;
+  d->batch = batch; d->heads_q = heads_q; d->heads_kv = heads_kv;
+  d->q_len = q_len; d->kv_len = kv_len; d->head_dim = head_dim;
+  d->k_layout = k_layout;
+  d->scale = 1.0f;
+  packed_strides(d->q_strides, heads_q, q_len, head_dim);
+  if (k_layout == FFAI_K_TRANSPOSED) packed_strides(d->k_strides, heads_kv, head_dim, kv_len);
+  else packed_strides(d->k_strides, heads_kv, kv_len, head_dim);
+  packed_strides(d->v_strides, heads_kv, kv_len, head_dim);
+  packed_strides(d->o_strides, heads_q, q_len, head_dim);
+}
+
+int ffai_attn_serves(const ffai_attn_desc* d) {
+  std::string why;
+  return check_desc(d, &why) == FFAI_OK ? 1 : 0;
+}
+
+int ffai_attn_workspace_bytes(const ffai_attn_desc* d, size_t* bytes) {
+  if (!bytes) return fail(FFAI_ERR_INVALID, "null bytes pointer");
+  *bytes = 0;
+  std::string why;
+  const int rc = check_desc(d, &why);
+  if (rc == FFAI_DECLINED) return fail(FFAI_DECLINED, "declined: " + why);
+  if (rc != FFAI_OK) return fail(rc, why);
+  *bytes = make_plan(d, true).ws_bytes;
+  return FFAI_OK;
+}
+
+int ffai_attn_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v,
+                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_fwd(d, q, k, v, out, workspace, workspace_bytes, stream, true);
+}
+
+int ffai_serves(const ffai_tensor* kt, const ffai_tensor* v) {
+  if (!kt || !v || !kt->on_device || !v->on_device) return 0;
+  if (kt->dims[0] != 1 || kt->dims[2] != kHD || v->dims[0] != 1 || v->dims[3] != kHD) return 0;
+  const int64_t keys = kt->dims[3];
+  return (kt->dims[1] == v->dims[1] && v->dims[2] == keys &&
+          keys >= std::max<int64_t>(kMinSeq, decode_min_keys()))
+             ? 1
+             : 0;
+}
+
+int ffai_attend_workspace_bytes(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
+                                size_t* bytes) {
+  if (!bytes) return fail(FFAI_ERR_INVALID, "null bytes pointer");
+  *bytes = 0;
+  if (!q || !kt || !v) return fail(FFAI_ERR_INVALID, "null tensor");
+  std::string why;
+  if (attend_accepts(q, kt, v, 0, &why) != FFAI_OK) return fail(FFAI_DECLINED, "declined: " + why);
+  ffai_attn_desc d;
+  attend_desc(q, kt, v, &d);
+  *bytes = make_plan(&d, true).ws_bytes;
+  return FFAI_OK;
+}
+
+int ffai_attend(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v, int masked,
+                ffai_tensor* out, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (!q || !kt || !v || !out) return fail(FFAI_ERR_INVALID, "null tensor");
+  std::string why;
+  if (attend_accepts(q, kt, v, masked, &why) != FFAI_OK) return fail(FFAI_DECLINED, "declined: " + why);
+  const int64_t heads = q->dims[1], qlen = q->dims[2];
+  // cpu_fwd's own checks (flash_attn.rs:289-296, 357-363): the f16 arm is the decode shape only;
+  // anything else that is not all-f32 and contiguous is an error, not a decline.
+  if (kt->dtype == FFAI_F16 && qlen != 1) return fail(FFAI_ERR_INVALID, "flash-attn: f32 only");
+  if (!contiguous(q) || !contiguous(kt) || !contiguous(v))
+    return fail(FFAI_ERR_INVALID, "flash-attn: contiguous operands only");
+  if (out->dtype != FFAI_F32 || !out->on_device || !dims_are(out, 1, heads, qlen, kHD) || !contiguous(out))
+    return fail(FFAI_ERR_INVALID, "out must be a contiguous f32 (1,H,qlen,64) device tensor");
+  ffai_attn_desc d;
+  attend_desc(q, kt, v, &d);
+  return run_fwd(&d, q->data, kt->data, v->data, out->data, workspace, workspace_bytes, stream, true);
+}
+
+int ffai_attend_merged(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
+                       ffai_tensor* out, void* stream) {
+  g_last_error.clear();
+  if (!q || !kt || !v || !out) return fail(FFAI_ERR_INVALID, "null tensor");
+  // attend_merged's accept set (flash_attn.rs:135-153)
+  const int64_t b = q->dims[0], heads = q->dims[1], qlen = q->dims[2], hd = q->dims[3];
+  if (b != 1 || hd != kHD || !q->on_device || !kt->on_device || !v->on_device)
+    return fail(FFAI_DECLINED, "declined: batch 1, head_dim 64, device tensors only");
+  if (q->dtype != FFAI_F32 || kt->dtype != FFAI_F32 || v->dtype != FFAI_F32)
+    return fail(FFAI_DECLINED, "declined: f32 only");
+  if (kt->dims[0] != 1 || kt->dims[1] != heads || kt->dims[2] != kHD)
+    return fail(FFAI_DECLINED, "declined: kt shape");
+  const int64_t keys = kt->dims[3];
+  if (!dims_are(v, 1, heads, keys, kHD) || qlen != keys || keys < kMinSeq)
+    return fail(FFAI_DECLINED, "declined: v shape, qlen != keys or keys < 256");
+  if (!contiguous(q) || !contiguous(kt) || !contiguous(v))
+    return fail(FFAI_ERR_INVALID, "flash-attn-merged: contiguous only");
+  if (out->dtype != FFAI_F32 || !out->on_device || !dims_are(out, 1, keys, heads * kHD, 1) ||
+      out->strides[0] != keys * heads * kHD || out->strides[1] != heads * kHD || out->strides[2] != 1)
+    return fail(FFAI_ERR_INVALID, "out must be a contiguous f32 (1,T,H*64) device tensor");
+  ffai_attn_desc d;
+  attend_desc(q, kt, v, &d);
+  // merged layout: row i of head h at i*H*64 + h*64
+  d.o_strides[0] = keys * heads * kHD;
+  d.o_strides[1] = kHD;
+  d.o_strides[2] = heads * kHD;
+  d.o_strides[3] = 1;
+  return run_fwd(&d, q->data, kt->data, v->data, out->data, nullptr, 0, stream, false);
+}
+
+int ffai_get_decode_min_keys(void) { return decode_min_keys(); }
+
+void ffai_set_decode_min_keys(int n) {
+  if (n >= 0) g_decode_min_keys.store(n, std::memory_order_relaxed);
+}
+
+const char* ffai_attn_last_error(void) { return g_last_error.c_str(); }
+
+int ffai_attn_abi_version(void) { return FFAI_ATTN_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,55 @@
+// Internal interface between the C ABI (attn_api.cpp) and the gfx950 kernels
+// (attn_kernels.hip). Not installed; callers use include/ffai_attn.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ffai {
+
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// Everything a forward launch needs, resolved by the host from an ffai_attn_desc.
+struct FwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* ws;              // split-key partials: [B][Hq][n_split][Tq][D] O then [..][2] (m, l)
+  const int32_t* kv_lens; // device int32[B] or nullptr
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;  // k_st: stride between key rows (rows layout) or d rows (K^T)
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int32_t B, Hq, Hkv, Tq, Tk;
+  int32_t causal, q_offset;
+  int32_t n_qblk;            // ceil(Tq / block_m)
+  int32_t n_split;           // key splits per (b, h, q-block); 1 = no partials
+  int32_t tiles_per_split;   // key tiles (of 64) per split
+  int32_t n_work;            // B * Hq * n_qblk * n_split logical workgroups
+  int32_t q_vec, k_vec, v_vec, o_vec;  // widest aligned access, in elements (1, 2, 4, 8)
+  float scale_log2;          // scale * log2(e)
+};
+
+struct CombineParams {
+  const float* ws;
+  void* o;
+  int64_t o_sb, o_sh, o_st;
+  int32_t B, Hq, Tq, n_split;
+  float scale_log2;
+};
+
+// Launchers; return hipSuccess or the launch error.
+// mode: kBF16 / kF16 (MFMA bf16/f16 kernel, q and kv the same 16-bit type) or kF32 (f32 MFMA
+// kernel; kv may be f32, f16 or bf16, widened to f32 as it is staged).
+// out_dtype: kF32, kF16 or kBF16. k_transposed: K^T layout.
+hipError_t launch_fwd(const FwdParams& p, int mode, int kv_dtype, int out_dtype, int head_dim,
+                      bool k_transposed, int waves, hipStream_t stream);
+hipError_t launch_combine(const CombineParams& p, int out_dtype, int head_dim,
+                          hipStream_t stream);
+
+// Query rows per workgroup for a kernel shape: 32 per wave.
+inline int block_m_for(int waves) { return 32 * waves; }
+constexpr int kBlockN = 64;  // keys per tile
+
+}  // namespace ffai

@@ -1,0 +1,226 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU oracle.
+
+Tolerances (max-abs): 1e-4 for f32, 2e-2 for bf16/f16 -- the bar stated for this path.
+bf16/f16 cases feed the oracle the SAME rounded values (upcast to f32), so the comparison
+measures the kernel's arithmetic, not the input rounding.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import textbook
+from ffai_amd import flash_attn as fa
+from tests.helpers import TOL_BF16, TOL_F32, max_abs, randn, round_bf16, round_f16
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x: np.ndarray, dtype, device) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device=device, dtype=dtype)
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------------------
+# Reference-surface mirrors (f32, batch 1, head_dim 64)
+# ---------------------------------------------------------------------------------------------
+
+def test_attend_matches_reference_unit_test_shape(gpu):
+    """flash_attn.rs:1005-1021 matches_three_op_path: H=4, T=512, f32, unscaled, < 1e-4."""
+    rng = np.random.default_rng(1005)
+    q, kt, v = randn(rng, (1, 4, 512, 64)), randn(rng, (1, 4, 64, 512)), randn(rng, (1, 4, 512, 64))
+    out = fa.attend(_dev(q, torch.float32, gpu), _dev(kt, torch.float32, gpu),
+                    _dev(v, torch.float32, gpu))
+    assert out is not None
+    got = _host(out)
+    want = oracle.attend_f32(q, kt, v)
+    three_op = textbook.attention(q, kt, v, k_transposed=True)
+    print("attend 4x512 f32: vs oracle", max_abs(got, want), "vs closed form", max_abs(got, three_op))
+    assert max_abs(got, want) < TOL_F32
+    assert max_abs(got, three_op) < TOL_F32
+
+
+@pytest.mark.parametrize("seq", [256, 300, 1500])
+def test_attend_merged_tiny_encoder(gpu, seq):
+    """MergedAttnOp at the whisper-tiny shape (6 heads) with scale 1/8 folded into q, as the
+    reference probe does (examples/flash_probe.rs:375-405); ragged tails at 300 and 1500."""
+    rng = np.random.default_rng(seq)
+    h = 6
+    q = randn(rng, (1, h, seq, 64)) * np.float32(1 / 8)
+    kt, v = randn(rng, (1, h, 64, seq)), randn(rng, (1, h, seq, 64))
+    out = fa.attend_merged(_dev(q, torch.float32, gpu), _dev(kt, torch.float32, gpu),
+                           _dev(v, torch.float32, gpu))
+    assert out is not None and tuple(out.shape) == (1, seq, h * 64)
+    got = _host(out)
+    want = oracle.attend_merged(q, kt, v)
+    err = max_abs(got, want)
+    print(f"attend_merged H6 T{seq}: {err:.3e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("keys", [8, 37, 448, 1500])
+def test_attend_decode_f32(gpu, keys):
+    """FlashAttnOp f32 decode arm (qlen == 1), xattn_head: 6 heads."""
+    rng = np.random.default_rng(keys)
+    q = randn(rng, (1, 6, 1, 64)) * np.float32(0.125)
+    kt, v = randn(rng, (1, 6, 64, keys)), randn(rng, (1, 6, keys, 64))
+    out = fa.attend(_dev(q, torch.float32, gpu), _dev(kt, torch.float32, gpu),
+                    _dev(v, torch.float32, gpu))
+    assert out is not None
+    err = max_abs(_host(out), oracle.attend_f32(q, kt, v))
+    print(f"decode f32 K{keys}: {err:.3e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("keys", [37, 1500])
+def test_attend_decode_f16_kv(gpu, keys):
+    """FlashAttnOp f16-K/V decode arm (xattn_head_f16): q f32, K/V f16, f32 math."""
+    rng = np.random.default_rng(100 + keys)
+    q = randn(rng, (1, 6, 1, 64)) * np.float32(0.125)
+    kt = randn(rng, (1, 6, 64, keys)).astype(np.float16)
+    v = randn(rng, (1, 6, keys, 64)).astype(np.float16)
+    out = fa.attend(_dev(q, torch.float32, gpu), _dev(kt, torch.float16, gpu),
+                    _dev(v, torch.float16, gpu))
+    assert out is not None
+    err = max_abs(_host(out), oracle.attend_f16kv(q, kt, v))
+    print(f"decode f16kv K{keys}: {err:.3e}")
+    assert err < TOL_F32
+
+
+# ---------------------------------------------------------------------------------------------
+# General descriptor path (extension of the reference: batch, bf16/f16, GQA, D=128, causal)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k_transposed", [True, False])
+@pytest.mark.parametrize("out_f32", [True, False])
+def test_encoder_16bit(gpu, dtype, k_transposed, out_f32):
+    """Encoder shape in bf16/f16 with K x 2 (the whisper-small stress case), ragged T=300."""
+    rng = np.random.default_rng(2)
+    b, h, t, d = 2, 3, 300, 64
+    rnd = round_bf16 if dtype == torch.bfloat16 else round_f16
+    q = rnd(randn(rng, (b, h, t, d)))
+    k = rnd(randn(rng, (b, h, t, d)) * np.float32(2.0))
+    v = rnd(randn(rng, (b, h, t, d)))
+    scale = d ** -0.5
+    kk = np.ascontiguousarray(np.swapaxes(k, 2, 3)) if k_transposed else k
+    out = fa.attention(_dev(q, dtype, gpu), _dev(kk, dtype, gpu), _dev(v, dtype, gpu),
+                       k_transposed=k_transposed, scale=scale,
+                       out_dtype=torch.float32 if out_f32 else dtype)
+    assert out is not None
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=scale)
+    err = max_abs(_host(out), want)
+    print(f"encoder {dtype} kt={k_transposed} f32out={out_f32}: {err:.3e}")
+    assert err < TOL_BF16
+
+
+def test_encoder_f32_batched_rows_layout(gpu):
+    rng = np.random.default_rng(3)
+    b, h, t, d = 2, 2, 700, 64
+    q, k, v = randn(rng, (b, h, t, d)), randn(rng, (b, h, t, d)), randn(rng, (b, h, t, d))
+    out = fa.attention(_dev(q, torch.float32, gpu), _dev(k, torch.float32, gpu),
+                       _dev(v, torch.float32, gpu), scale=0.125)
+    err = max_abs(_host(out), oracle.attend_general(q, k, v, k_transposed=False, scale=0.125))
+    print(f"encoder f32 rows: {err:.3e}")
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_causal_gqa(gpu, d):
+    """Causal prefill with grouped K/V heads (Hq=4, Hkv=2), S=130 (ragged), bf16."""
+    rng = np.random.default_rng(5 + d)
+    b, hq, hkv, s = 1, 4, 2, 130
+    q = round_bf16(randn(rng, (b, hq, s, d)))
+    k = round_bf16(randn(rng, (b, hkv, s, d)))
+    v = round_bf16(randn(rng, (b, hkv, s, d)))
+    scale = d ** -0.5
+    out = fa.attention(_dev(q, torch.bfloat16, gpu), _dev(k, torch.bfloat16, gpu),
+                       _dev(v, torch.bfloat16, gpu), scale=scale, causal=True,
+                       out_dtype=torch.float32)
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=scale, causal=True)
+    err = max_abs(_host(out), want)
+    print(f"causal gqa d{d}: {err:.3e}")
+    assert err < TOL_BF16
+
+
+def test_causal_with_offset(gpu):
+    """Prompt-continuation shape: 40 new queries at absolute offset 90 over 130 keys."""
+    rng = np.random.default_rng(9)
+    b, h, tq, tk, d = 2, 2, 40, 130, 64
+    q = round_bf16(randn(rng, (b, h, tq, d)))
+    k = round_bf16(randn(rng, (b, h, tk, d)))
+    v = round_bf16(randn(rng, (b, h, tk, d)))
+    out = fa.attention(_dev(q, torch.bfloat16, gpu), _dev(k, torch.bfloat16, gpu),
+                       _dev(v, torch.bfloat16, gpu), scale=0.125, causal=True, q_offset=90,
+                       out_dtype=torch.float32)
+    want = textbook.attention(q, k, v, scale=0.125, causal=True, q_offset=90)
+    err = max_abs(_host(out), want)
+    print(f"causal offset: {err:.3e}")
+    assert err < TOL_BF16
+
+
+def test_beam_cross_attention_shared_kv(gpu):
+    """Beam-search cross-attention: 5 beams read ONE K/V of 1500 frames; the beams are the query
+    rows of a single batch item, so K/V streams once (whisper-medium: 16 heads)."""
+    rng = np.random.default_rng(3)
+    beams, h, t, d = 5, 16, 1500, 64
+    q = round_bf16(randn(rng, (beams, h, 1, d)))
+    kt = round_bf16(randn(rng, (1, h, d, t)))
+    v = round_bf16(randn(rng, (1, h, t, d)))
+    qd = _dev(q, torch.bfloat16, gpu)
+    out = torch.empty(beams, h, 1, d, dtype=torch.float32, device=gpu)
+    # (beams, H, 1, D) viewed as (1, H, beams, D): beam rows H*D apart
+    res = fa.attention(qd.permute(2, 1, 0, 3), _dev(kt, torch.bfloat16, gpu),
+                       _dev(v, torch.bfloat16, gpu), k_transposed=True, scale=0.125,
+                       out=out.permute(2, 1, 0, 3))
+    assert res is not None
+    want = oracle.attend_general(np.swapaxes(q, 0, 2), kt, v, k_transposed=True, scale=0.125)
+    err = max_abs(_host(out), np.swapaxes(want, 0, 2))
+    print(f"beam cross-attn: {err:.3e}")
+    assert err < TOL_BF16
+
+
+def test_beam_self_attention_ragged(gpu):
+    """Decoder self-attention: 5 beams, each with its own cache of L_b keys (capacity 448)."""
+    rng = np.random.default_rng(33)
+    beams, h, cap, d = 5, 16, 448, 64
+    lens = np.array([1, 9, 200, 447, 448], np.int32)
+    q = round_bf16(randn(rng, (beams, h, 1, d)))
+    k = round_bf16(randn(rng, (beams, h, cap, d)))
+    v = round_bf16(randn(rng, (beams, h, cap, d)))
+    out = fa.attention(_dev(q, torch.bfloat16, gpu), _dev(k, torch.bfloat16, gpu),
+                       _dev(v, torch.bfloat16, gpu), scale=0.125,
+                       kv_lens=torch.from_numpy(lens).to(gpu), out_dtype=torch.float32)
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=0.125, kv_lens=lens)
+    err = max_abs(_host(out), want)
+    print(f"beam self-attn ragged: {err:.3e}")
+    assert err < TOL_BF16
+
+
+def test_whisper_large_shape_sampled_rows(gpu):
+    """Full whisper-large-v3 layer shape (B16 H20 T1500 bf16): every row computed on the GPU,
+    sampled rows checked against the float64 closed form on the same rounded inputs."""
+    rng = np.random.default_rng(4)
+    b, h, t, d = 16, 20, 1500, 64
+    g = torch.Generator(device="cpu").manual_seed(4)
+    q = torch.randn(b, h, t, d, generator=g).to(torch.bfloat16)
+    kt = torch.randn(b, h, d, t, generator=g).to(torch.bfloat16)
+    v = torch.randn(b, h, t, d, generator=g).to(torch.bfloat16)
+    out = fa.attention(q.to(gpu), kt.to(gpu), v.to(gpu), k_transposed=True, scale=0.125,
+                       out_dtype=torch.bfloat16)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    rows = np.sort(rng.choice(t, size=24, replace=False))
+    rows[0], rows[-1] = 0, t - 1
+    bi = [0, 7, 15]
+    want = textbook.attention(q[bi].float().numpy(), kt[bi].float().numpy(),
+                              v[bi].float().numpy(), k_transposed=True, scale=0.125, rows=rows)
+    err = max_abs(got[bi][:, :, rows], want)
+    print(f"large-v3 sampled rows: {err:.3e}")
+    assert err < TOL_BF16
