@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused attention path on one MI355X.
+
+Headline (``value``): encoder self-attention throughput at the whisper-large-v3 shape -- batch 16,
+20 heads, T = 1500, head_dim 64, bf16, non-causal, K given transposed (the reference's layout),
+scale 1/8 -- over the 32 encoder layers with distinct buffers per layer. One step = the 32 layer
+calls. FLOP = 4 * B * H * T^2 * D per layer (flash_probe.rs:432's convention).
+
+Also reported: the beam-5 decode step at the whisper-medium shape (24 layers of decoder
+self-attention over ragged per-beam caches plus cross-attention over 1500 shared encoder frames,
+bf16 K/V, f32 output), the whisper-tiny f32 encoder, and the CPU oracle (the reference's
+algorithm restated in C++/AVX2) timed on this host's cores on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+PEAK_F32_TFLOPS = 157.3     # MI355X fp32 matrix
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-extras", action="store_true")
+    ap.add_argument("--layers", type=int, default=32)
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------------------------------
+# Encoder (headline)
+# ------------------------------------------------------------------------------------------
+
+def encoder_bench(torch, fa, steps, warmup, layers, B=16, H=20, T=1500, D=64,
+                  dtype="bf16"):
+    dev = torch.device("cuda:0")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    g = torch.Generator(device=dev).manual_seed(4)
+    bufs = []
+    for _ in range(layers):
+        q = torch.randn(B, H, T, D, generator=g, device=dev).to(tdt)
+        kt = torch.randn(B, H, D, T, generator=g, device=dev).to(tdt)
+        v = torch.randn(B, H, T, D, generator=g, device=dev).to(tdt)
+        o = torch.empty(B, H, T, D, device=dev, dtype=tdt)
+        bufs.append((q, kt, v, o))
+    scale = D ** -0.5
+    ws = None
+    nbytes = fa.workspace_bytes(*bufs[0], k_transposed=True, scale=scale)
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    def step():
+        for q, kt, v, o in bufs:
+            r = fa.attention(q, kt, v, k_transposed=True, scale=scale, out=o, workspace=ws)
+            assert r is not None
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    flop_layer = 4.0 * B * H * T * T * D
+    launches = steps * layers
+    avg_launch_s = gpu_ms * 1e-3 / launches
+    return {
+        "elapsed_s": wall,
+        "gpu_ms": gpu_ms,
+        "ms_per_step": gpu_ms / steps,
+        "tflops": flop_layer * launches / (gpu_ms * 1e-3) / 1e12,
+        "flop_per_launch": flop_layer,
+        "avg_launch_us": avg_launch_s * 1e6,
+        "bytes_per_launch": 4.0 * B * H * T * D * (2 if dtype == "bf16" else 4),
+    }
+
+
+# ------------------------------------------------------------------------------------------
+# Beam-5 decode step (whisper-medium: 24 layers, 16 heads, D=64)
+# ------------------------------------------------------------------------------------------
+
+def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24,
+                 sets=3):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(3)
+    lens_cpu = torch.randint(1, cap + 1, (layers, beams), generator=g, dtype=torch.int32)
+    gd = torch.Generator(device=dev).manual_seed(3)
+    scale = D ** -0.5
+    bf = torch.bfloat16
+    all_sets = []
+    for _ in range(sets):   # > 2 x 256 MB: consecutive steps never find their K/V in the MALL
+        layer_bufs = []
+        for l in range(layers):
+            q_self = torch.randn(beams, H, 1, D, generator=gd, device=dev).to(bf)
+            k_self = torch.randn(beams, H, cap, D, generator=gd, device=dev).to(bf)
+            v_self = torch.randn(beams, H, cap, D, generator=gd, device=dev).to(bf)
+            lens = lens_cpu[l].to(dev)
+            q_x = torch.randn(beams, H, 1, D, generator=gd, device=dev).to(bf)
+            kt_x = torch.randn(1, H, D, T_enc, generator=gd, device=dev).to(bf)
+            v_x = torch.randn(1, H, T_enc, D, generator=gd, device=dev).to(bf)
+            o_self = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
+            o_x = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
+            layer_bufs.append((q_self, k_self, v_self, lens, o_self, q_x, kt_x, v_x, o_x))
+        all_sets.append(layer_bufs)
+    # workspaces (one per call site, reused across layers: calls are stream-ordered)
+    qs, ks, vs, ls, os_, qx, ktx, vx, ox = all_sets[0][0]
+    ws_self = torch.empty(max(1, fa.workspace_bytes(qs, ks, vs, os_, scale=scale, kv_lens=ls)),
+                          dtype=torch.uint8, device=dev)
+    ws_x = torch.empty(max(1, fa.workspace_bytes(qx.permute(2, 1, 0, 3), ktx, vx,
+                                                 ox.permute(2, 1, 0, 3), k_transposed=True,
+                                                 scale=scale)), dtype=torch.uint8, device=dev)
+
+    def step(layer_bufs):
+        for (q_self, k_self, v_self, lens, o_self, q_x, kt_x, v_x, o_x) in layer_bufs:
+            fa.attention(q_self, k_self, v_self, scale=scale, kv_lens=lens, out=o_self,
+                         workspace=ws_self)
+            fa.attention(q_x.permute(2, 1, 0, 3), kt_x, v_x, k_transposed=True, scale=scale,
+                         out=o_x.permute(2, 1, 0, 3), workspace=ws_x)
+
+    # capture one HIP graph per buffer set: the step's 48 attention calls replay without
+    # host-side dispatch (the kernels use no memset; the workspaces are preallocated)
+    graphs = []
+    step(all_sets[0])
+    torch.cuda.synchronize()
+    for s in range(sets):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            step(all_sets[s])
+        graphs.append(gr)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs[i % sets].replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        graphs[i % sets].replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    gpu_ms = e0.elapsed_time(e1)
+    us_step = gpu_ms * 1e3 / steps
+    kv_row = H * D * 2 * 2  # K + V bytes per key (bf16)
+    cross_bytes = layers * (H * T_enc * D * 2 * 2 + beams * H * D * 2 + beams * H * D * 4)
+    self_bytes = int(lens_cpu.sum()) * kv_row + layers * (beams * H * D * 2 + beams * H * D * 4)
+    step_bytes = cross_bytes + self_bytes
+    return {
+        "us_per_step": us_step,
+        "bytes_per_step": step_bytes,
+        "cross_bytes_per_layer": cross_bytes / layers,
+        "self_bytes_per_step": self_bytes,
+        "gbps": step_bytes / (us_step * 1e-6) / 1e9,
+        "hbm_frac": step_bytes / (us_step * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+        "launches_per_step": 2 * layers * 2,
+        "mean_self_len": float(lens_cpu.float().mean()),
+        "buffer_sets": sets,
+    }
+
+
+# ------------------------------------------------------------------------------------------
+# CPU baseline: the oracle (reference algorithm restated) on this host's cores
+# ------------------------------------------------------------------------------------------
+
+def cpu_baseline(H=20, T=1500, D=64, budget_s=12.0):
+    import numpy as np
+
+    import oracle
+
+    oracle.build()
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    rng = np.random.default_rng(4)
+    q = oracle.round_bf16(rng.standard_normal((1, H, T, D)).astype(np.float32)) * np.float32(0.125)
+    kt = oracle.round_bf16(rng.standard_normal((1, H, D, T)).astype(np.float32))
+    v = oracle.round_bf16(rng.standard_normal((1, H, T, D)).astype(np.float32))
+    oracle.attend_f32(q, kt, v, threads=threads)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < 3:
+        t0 = time.perf_counter()
+        oracle.attend_f32(q, kt, v, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 41:
+            break
+    med = float(np.median(times))
+    flop = 4.0 * H * T * T * D
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": flop / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"one batch item of one whisper-large-v3 encoder layer: {H} heads x T={T}, "
+                   f"D={D}, bf16-rounded inputs in f32 math (the reference kernel's dtype); "
+                   f"median of {len(times)} runs, {med * 1e3:.1f} ms each; "
+                   f"heads over {threads} threads as rayon does; CPU: {cpu_model}"),
+    }
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"{args.gpus}). The attention shards over (batch, head) with no exchange; see "
+              f"DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from ffai_amd import flash_attn as fa
+    from ffai_amd import _lib
+
+    _lib.load()
+    log("encoder: whisper-large-v3 bf16 ...")
+    enc = encoder_bench(torch, fa, args.steps, args.warmup, args.layers)
+    log(f"encoder: {enc['tflops']:.1f} TFLOP/s, {enc['ms_per_step']:.3f} ms/step")
+    extras = {}
+    if not args.skip_extras:
+        log("decode: beam-5 whisper-medium step ...")
+        dec = decode_bench(torch, fa, max(args.steps * 10, 100), 10)
+        log(f"decode: {dec['us_per_step']:.1f} us/step, {dec['gbps']:.0f} GB/s")
+        extras["decode_beam5"] = dec
+        log("encoder: whisper-tiny f32 ...")
+        tiny = encoder_bench(torch, fa, max(args.steps * 5, 50), args.warmup, 4, B=1, H=6,
+                             dtype="f32")
+        tiny["frac_of_f32_peak"] = tiny["tflops"] / PEAK_F32_TFLOPS
+        extras["encoder_tiny_f32"] = tiny
+        log(f"tiny f32: {tiny['tflops']:.2f} TFLOP/s")
+        log("encoder: whisper-small bf16 ...")
+        small = encoder_bench(torch, fa, args.steps, args.warmup, 4, B=8, H=12)
+        extras["encoder_small_bf16"] = small
+        log(f"small bf16: {small['tflops']:.1f} TFLOP/s")
+    cpu = None
+    if not args.skip_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline()
+        log(f"cpu: {cpu['value'] * 1e3:.1f} GFLOP/s on {cpu['cores']} threads")
+
+    achieved = enc["flop_per_launch"] / (enc["avg_launch_us"] * 1e-6) / 1e12
+    line = {
+        "metric": "attention TFLOP/s + % MFMA peak (encoder); decode-step us + HBM GB/s (beam 5)",
+        "value": round(enc["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(enc["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V ~ N(0,1) from seed 4, K given transposed (B,H,D,T)",
+        "config": {"workload": "whisper-large-v3 encoder self-attention", "batch": 16,
+                   "heads": 20, "seq": 1500, "head_dim": 64, "layers": args.layers,
+                   "causal": False, "scale": 0.125, "k_layout": "transposed",
+                   "out_dtype": "bf16"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": load_traffic("encoder_large_v3_bf16")},
+        "cpu_baseline": cpu,
+    }
+    if extras:
+        line["extras"] = extras
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

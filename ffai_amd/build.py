@@ -15,7 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libffai_attn.so")
-SOURCES = [os.path.join(CSRC, "attn_kernels.hip"), os.path.join(CSRC, "attn_api.cpp")]
+BUILD_DIR = os.path.join(HERE, "_build")
+SOURCES = [os.path.join(CSRC, n) for n in
+           ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "attn_launch.hip", "attn_api.cpp")]
 ARCH = "gfx950"
 
 
@@ -28,7 +30,7 @@ def hipcc() -> str:
 
 def flags() -> list[str]:
     return [
-        "-O3", "-std=c++17", "-fPIC", "-shared",
+        "-O3", "-std=c++17", "-fPIC",
         f"--offload-arch={ARCH}",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"),
@@ -36,22 +38,34 @@ def flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source into LIB_PATH (always recompiles). Returns the library path."""
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc()] + flags()
-    # hipcc compiles .cpp as host C++ unless told otherwise; the API file calls the HIP runtime
-    # only, so it is fine either way, but force HIP language for the .hip source.
-    cmd += ["-x", "hip", SOURCES[0], "-x", "hip", SOURCES[1], "-o", tmp]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every source (always) into objects in parallel, then link LIB_PATH."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    cc = hipcc()
+    objs, cmds = [], []
+    for src in SOURCES:
+        obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append([cc] + flags() + ["-c", "-x", "hip", src, "-o", obj])
+    jobs = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 8)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB_PATH + ".tmp"
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -21,6 +21,8 @@
 //   * Few-query shapes (decode) split the keys over workgroups; partial (O, m, l) go to the
 //     workspace and combine_kernel merges them by log-sum-exp.
 
+#pragma once
+
 #include "attn_kernels.h"
 
 #include <type_traits>
@@ -559,80 +561,5 @@ __global__ __launch_bounds__(64) void combine_kernel(CombineParams p) {
   }
 }
 
-template <int MODE, int KVT, int OUTT, int D, bool KT, int NW>
-hipError_t launch_one(const FwdParams& p, hipStream_t s) {
-  const unsigned grid = (unsigned)((p.n_work + 7) / 8 * 8);
-  hipLaunchKernelGGL((fwd_kernel<MODE, KVT, OUTT, D, KT, NW>), dim3(grid), dim3(NW * 64), 0, s,
-                     p);
-  return hipGetLastError();
-}
-
-template <int MODE, int KVT, int OUTT, int D, bool KT>
-hipError_t pick_waves(const FwdParams& p, int waves, hipStream_t s) {
-  switch (waves) {
-    case 1: return launch_one<MODE, KVT, OUTT, D, KT, 1>(p, s);
-    case 4: return launch_one<MODE, KVT, OUTT, D, KT, 4>(p, s);
-    default: return hipErrorInvalidValue;
-  }
-}
-
-template <int MODE, int KVT, int OUTT, int D>
-hipError_t pick_layout(const FwdParams& p, bool kt, int waves, hipStream_t s) {
-  return kt ? pick_waves<MODE, KVT, OUTT, D, true>(p, waves, s)
-            : pick_waves<MODE, KVT, OUTT, D, false>(p, waves, s);
-}
-
-template <int MODE, int KVT, int OUTT>
-hipError_t pick_dim(const FwdParams& p, int d, bool kt, int waves, hipStream_t s) {
-  if (d == 64) return pick_layout<MODE, KVT, OUTT, 64>(p, kt, waves, s);
-  if constexpr (MODE != kF32) {
-    if (d == 128) return pick_layout<MODE, KVT, OUTT, 128>(p, kt, waves, s);
-  }
-  return hipErrorInvalidValue;
-}
-
 }  // namespace
-
-hipError_t launch_fwd(const FwdParams& p, int mode, int kv_dtype, int out_dtype, int head_dim,
-                      bool k_transposed, int waves, hipStream_t stream) {
-  if (mode == kBF16) {
-    if (kv_dtype != kBF16) return hipErrorInvalidValue;
-    if (out_dtype == kBF16) return pick_dim<kBF16, kBF16, kBF16>(p, head_dim, k_transposed, waves, stream);
-    if (out_dtype == kF32) return pick_dim<kBF16, kBF16, kF32>(p, head_dim, k_transposed, waves, stream);
-    return hipErrorInvalidValue;
-  }
-  if (mode == kF16) {
-    if (kv_dtype != kF16) return hipErrorInvalidValue;
-    if (out_dtype == kF16) return pick_dim<kF16, kF16, kF16>(p, head_dim, k_transposed, waves, stream);
-    if (out_dtype == kF32) return pick_dim<kF16, kF16, kF32>(p, head_dim, k_transposed, waves, stream);
-    return hipErrorInvalidValue;
-  }
-  if (mode == kF32 && out_dtype == kF32) {
-    if (kv_dtype == kF32) return pick_dim<kF32, kF32, kF32>(p, head_dim, k_transposed, waves, stream);
-    if (kv_dtype == kF16) return pick_dim<kF32, kF16, kF32>(p, head_dim, k_transposed, waves, stream);
-    if (kv_dtype == kBF16) return pick_dim<kF32, kBF16, kF32>(p, head_dim, k_transposed, waves, stream);
-  }
-  return hipErrorInvalidValue;
-}
-
-hipError_t launch_combine(const CombineParams& p, int out_dtype, int head_dim,
-                          hipStream_t stream) {
-  const dim3 grid((unsigned)(p.B * p.Hq * p.Tq));
-#define FFAI_COMBINE(OT, DD) \
-  hipLaunchKernelGGL((combine_kernel<OT, DD>), grid, dim3(64), 0, stream, p)
-  if (head_dim == 64) {
-    if (out_dtype == kF32) FFAI_COMBINE(kF32, 64);
-    else if (out_dtype == kBF16) FFAI_COMBINE(kBF16, 64);
-    else FFAI_COMBINE(kF16, 64);
-  } else if (head_dim == 128) {
-    if (out_dtype == kF32) FFAI_COMBINE(kF32, 128);
-    else if (out_dtype == kBF16) FFAI_COMBINE(kBF16, 128);
-    else FFAI_COMBINE(kF16, 128);
-  } else {
-    return hipErrorInvalidValue;
-  }
-#undef FFAI_COMBINE
-  return hipGetLastError();
-}
-
 }  // namespace ffai

@@ -47,6 +47,13 @@ hipError_t launch_fwd(const FwdParams& p, int mode, int kv_dtype, int out_dtype,
                       bool k_transposed, int waves, hipStream_t stream);
 hipError_t launch_combine(const CombineParams& p, int out_dtype, int head_dim,
                           hipStream_t stream);
+// Per-dtype instantiation units (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip).
+hipError_t launch_fwd_bf16(const FwdParams& p, int out_dtype, int d, bool kt, int waves,
+                           hipStream_t s);
+hipError_t launch_fwd_f16(const FwdParams& p, int out_dtype, int d, bool kt, int waves,
+                          hipStream_t s);
+hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int waves,
+                          hipStream_t s);
 
 // Query rows per workgroup for a kernel shape: 32 per wave.
 inline int block_m_for(int waves) { return 32 * waves; }

@@ -27,7 +27,11 @@ _DT = {torch.float32: L.F32, torch.float16: L.F16, torch.bfloat16: L.BF16}
 _TORCH_DT = {v: k for k, v in _DT.items()}
 
 
-def _stream_handle() -> ctypes.c_void_p:
+def _stream_handle(t: Optional[torch.Tensor] = None) -> ctypes.c_void_p:
+    """The caller's current HIP stream (None for host tensors, which the library declines
+    before touching any stream)."""
+    if t is not None and not t.is_cuda:
+        return ctypes.c_void_p(None)
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
@@ -75,7 +79,7 @@ def attend(q: torch.Tensor, kt: torch.Tensor, v: torch.Tensor,
         # let the C mirror apply (and report) the decline, exactly as it would for a caller
         out = torch.empty(0, device=q.device)
         rc = lib.ffai_attend(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), int(masked),
-                             ctypes.byref(_view(out)), None, 0, _stream_handle())
+                             ctypes.byref(_view(out)), None, 0, _stream_handle(q))
         return None if L.check(rc) == L.FFAI_DECLINED else out
     L.check(rc)
     out = torch.empty(q.shape[0], q.shape[1], q.shape[2], 64, dtype=torch.float32,
@@ -97,7 +101,7 @@ def attend_merged(q: torch.Tensor, kt: torch.Tensor,
     out = torch.empty(1, seq, heads * 64, dtype=torch.float32, device=q.device)
     rc = lib.ffai_attend_merged(ctypes.byref(_view(q)), ctypes.byref(_view(kt)),
                                 ctypes.byref(_view(v)), ctypes.byref(_view(out)),
-                                _stream_handle())
+                                _stream_handle(q))
     if L.check(rc) == L.FFAI_DECLINED:
         return None
     return out

@@ -32,7 +32,7 @@ from . import textbook  # noqa: F401  (re-export)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
-_VERSION = 3
+_VERSION = 4
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -64,8 +64,16 @@ def lib():
         L.oracle_attend_general.argtypes = (
             [ctypes.c_int] * 6 + [_f32p, _f32p, ctypes.c_int, _f32p, _f32p, ctypes.c_float,
                                   ctypes.c_int, ctypes.c_int, _i32p, ctypes.c_int])
+        L.oracle_plant_fault.argtypes = [ctypes.c_int]
+        L.oracle_plant_fault.restype = None
         _lib = L
     return _lib
+
+
+def plant_fault(kind: int) -> None:
+    """Tests only: make the oracle commit a known mistake (1 skip rescale, 2 drop the degree-5
+    exp term, 3 drop each tile's last key, 4 transposed K index); 0 restores it."""
+    lib().oracle_plant_fault(int(kind))
 
 
 def _f32(a: np.ndarray) -> np.ndarray:

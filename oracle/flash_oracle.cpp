@@ -36,6 +36,11 @@ constexpr int kHD = 64;   // head_dim of the reference  (flash_attn.rs:50)
 
 constexpr float kNegInf = -std::numeric_limits<float>::infinity();
 
+// Planted mistakes, for the tests that prove the oracle's checks can fail (never set otherwise):
+// 1 = skip the accumulator rescale, 2 = drop the degree-5 term of the exp polynomial,
+// 3 = lose the last key of every tile, 4 = use K^T's row instead of its column (transposed index).
+int g_fault = 0;
+
 // ---------------------------------------------------------------------------------------------
 // Vector primitives: flash_attn.rs:545-593.
 // exp(x) = 2^(x*log2 e): the rounded integer part goes straight into the exponent field, the
@@ -49,7 +54,7 @@ __attribute__((target("avx2,fma"))) inline __m256 vexp(__m256 x) {
   // Horner over the polynomial coefficients of flash_attn.rs:559-564, highest degree first.
   static const float kC[6] = {0.0013333558f, 0.009618129f, 0.05550411f,
                               0.2402265f,    0.6931472f,   1.0f};
-  __m256 poly = _mm256_set1_ps(kC[0]);
+  __m256 poly = _mm256_set1_ps(g_fault == 2 ? 0.0f : kC[0]);
   for (int i = 1; i < 6; ++i) poly = _mm256_fmadd_ps(poly, f, _mm256_set1_ps(kC[i]));
   const __m256i bits =
       _mm256_slli_epi32(_mm256_add_epi32(_mm256_cvtps_epi32(n), _mm256_set1_epi32(127)), 23);
@@ -213,13 +218,20 @@ __attribute__((target("avx2,fma"))) void encoder_head(const float* q, const floa
     std::fill(run_sum.begin(), run_sum.begin() + rows, 0.0f);
     const float* qb = q + (long)q0 * kHD;
     for (int k0 = 0; k0 < seq; k0 += kBK) {
-      const int cols = std::min(kBK, seq - k0);
+      const int cols = std::min(kBK, seq - k0) - (g_fault == 3 ? 1 : 0);
       scores_block<kHD>(qb, kHD, kt, seq, k0, rows, cols, scores.data());
+      if (g_fault == 4)  // read K^T[j, t] instead of K^T[t, j] (square tiles only)
+        for (int i = 0; i < rows; ++i)
+          for (int j = 0; j < cols; ++j) {
+            float a = 0.0f;
+            for (int t = 0; t < kHD; ++t) a += qb[i * kHD + t] * kt[(long)(k0 + j) * seq + t];
+            scores[i * kBK + j] = a;
+          }
       for (int i = 0; i < rows; ++i) {
         const RowStep st = softmax_step(&scores[i * kBK], cols, run_max[i]);
         run_sum[i] = std::fma(run_sum[i], st.correction, st.block_sum);
         run_max[i] = st.new_max;
-        if (st.correction != 1.0f)
+        if (st.correction != 1.0f && g_fault != 1)
           for (int d = 0; d < kHD; ++d) acc[i * kHD + d] *= st.correction;
       }
       pv_block<kHD>(scores.data(), v, kHD, acc.data(), rows, k0, cols);
@@ -381,7 +393,10 @@ __attribute__((target("avx2,fma"))) void general_head(const float* q, long q_row
 extern "C" {
 
 // Version tag so a stale build is detectable from Python.
-int oracle_version() { return 3; }
+int oracle_version() { return 4; }
+
+// Test hook: plant one of the mistakes listed at g_fault (0 restores the faithful oracle).
+void oracle_plant_fault(int kind) { g_fault = kind; }
 
 // exp polynomial of flash_attn.rs:553-571 on n floats (tails padded internally).
 __attribute__((target("avx2,fma"))) void oracle_exp_poly(const float* x, float* y, long n) {

@@ -1,0 +1,210 @@
+"""C ABI and host logic on the CPU (no GPU calls): the library loads and exports every symbol the
+header declares, descriptors initialise as documented, the serves predicate and the decline
+contract of the reference's attend / attend_merged / serves hold (flash_attn.rs:103-264,
+1024-1039)."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from ffai_amd import _lib as L
+
+FAKE = 0x10000  # a non-null "device" address: no test below reaches a HIP call
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return L.load()
+
+
+def view(dims, dtype=L.F32, on_device=1, strides=None, data=FAKE):
+    v = L.TensorView()
+    v.data = data
+    v.dtype = dtype
+    v.on_device = on_device
+    dims = list(dims) + [1] * (4 - len(dims))
+    if strides is None:
+        strides = [0] * 4
+        acc = 1
+        for i in range(3, -1, -1):
+            strides[i] = acc
+            acc *= dims[i]
+    for i in range(4):
+        v.dims[i] = dims[i]
+        v.strides[i] = strides[i]
+    return v
+
+
+def attend_rc(lib, q, kt, v, masked=0, out=None):
+    out = out or view((q.dims[0], q.dims[1], q.dims[2], 64))
+    return lib.ffai_attend(ctypes.byref(q), ctypes.byref(kt), ctypes.byref(v), masked,
+                           ctypes.byref(out), None, 0, None)
+
+
+def test_exports_every_header_symbol(lib):
+    names = L.header_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.ffai_attn_abi_version() == L.ABI_VERSION
+
+
+def test_desc_init_packed_strides(lib):
+    d = L.AttnDesc()
+    lib.ffai_attn_desc_init(ctypes.byref(d), L.BF16, L.BF16, L.BF16, 2, 12, 2, 100, 300, 128,
+                            L.K_TRANSPOSED)
+    assert list(d.q_strides) == [12 * 100 * 128, 100 * 128, 128, 1]
+    assert list(d.k_strides) == [2 * 128 * 300, 128 * 300, 300, 1]
+    assert list(d.v_strides) == [2 * 300 * 128, 300 * 128, 128, 1]
+    assert list(d.o_strides) == [12 * 100 * 128, 100 * 128, 128, 1]
+    assert d.scale == 1.0 and d.causal == 0 and not d.kv_lens
+    lib.ffai_attn_desc_init(ctypes.byref(d), L.F32, L.F32, L.F32, 1, 1, 1, 5, 7, 64, L.K_ROWS)
+    assert list(d.k_strides) == [7 * 64, 7 * 64, 64, 1]
+
+
+def desc(lib, qd, kvd, od, b, hq, hkv, tq, tk, d, layout=L.K_ROWS):
+    x = L.AttnDesc()
+    lib.ffai_attn_desc_init(ctypes.byref(x), qd, kvd, od, b, hq, hkv, tq, tk, d, layout)
+    return x
+
+
+@pytest.mark.parametrize("args,served", [
+    ((L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64), True),
+    ((L.BF16, L.BF16, L.F32, 1, 12, 2, 4096, 4096, 128), True),
+    ((L.F16, L.F16, L.F16, 1, 4, 4, 10, 10, 64), True),
+    ((L.F32, L.F32, L.F32, 1, 6, 6, 1500, 1500, 64), True),
+    ((L.F32, L.F16, L.F32, 1, 6, 6, 1, 1500, 64), True),   # reference f16-K/V decode arm
+    ((L.F32, L.BF16, L.F32, 5, 16, 16, 1, 448, 64), True),
+    ((L.F32, L.F32, L.F32, 1, 6, 6, 100, 100, 128), False),  # f32 serves head_dim 64 only
+    ((L.BF16, L.F32, L.BF16, 1, 6, 6, 100, 100, 64), False),  # mixed 16-bit/f32
+    ((L.BF16, L.BF16, L.F16, 1, 6, 6, 100, 100, 64), False),  # bf16 in, f16 out
+    ((L.BF16, L.BF16, L.BF16, 1, 6, 6, 100, 100, 96), False),  # head_dim 96
+])
+def test_serves_predicate(lib, args, served):
+    d = desc(lib, *args)
+    assert lib.ffai_attn_serves(ctypes.byref(d)) == int(served)
+    n = ctypes.c_size_t(0)
+    rc = lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n))
+    assert rc == (L.FFAI_OK if served else L.FFAI_DECLINED)
+
+
+def test_fwd_declines_and_rejects_without_touching_the_gpu(lib):
+    d = desc(lib, L.BF16, L.BF16, L.BF16, 1, 6, 6, 100, 100, 96)
+    assert lib.ffai_attn_fwd(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_DECLINED
+    d = desc(lib, L.BF16, L.BF16, L.BF16, 1, 6, 4, 100, 100, 64)  # 6 % 4 != 0
+    assert lib.ffai_attn_fwd(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_ERR_INVALID
+    d = desc(lib, L.BF16, L.BF16, L.BF16, 1, 6, 6, 100, 100, 64)
+    d.scale = -1.0
+    assert lib.ffai_attn_fwd(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_ERR_INVALID
+    assert "scale" in L.last_error()
+    d = desc(lib, L.BF16, L.BF16, L.BF16, 1, 6, 6, 100, 100, 64)
+    d.q_strides[3] = 2
+    assert lib.ffai_attn_fwd(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_ERR_INVALID
+    d = desc(lib, L.BF16, L.BF16, L.BF16, 1, 6, 6, 100, 100, 64)
+    assert lib.ffai_attn_fwd(ctypes.byref(d), None, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_ERR_INVALID
+
+
+def test_workspace_only_for_split_shapes(lib):
+    n = ctypes.c_size_t(0)
+    big = desc(lib, L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED)
+    assert lib.ffai_attn_workspace_bytes(ctypes.byref(big), ctypes.byref(n)) == L.FFAI_OK
+    assert n.value == 0
+    beam = desc(lib, L.BF16, L.BF16, L.F32, 1, 16, 16, 5, 1500, 64, L.K_TRANSPOSED)
+    assert lib.ffai_attn_workspace_bytes(ctypes.byref(beam), ctypes.byref(n)) == L.FFAI_OK
+    assert n.value > 0 and n.value % (5 * 16 * 66 * 4) == 0
+
+
+# ---------------------------------------------------------------------------------------------
+# the reference's decline contract (flash_attn.rs:218-264, 1024-1039)
+# ---------------------------------------------------------------------------------------------
+
+def test_declines_unsupported_shapes_like_the_reference(lib):
+    """flash_attn.rs:1024-1039: qlen 1 with 1 key, and masked attention, both decline."""
+    q, kt, v = view((1, 4, 1, 64)), view((1, 4, 64, 1)), view((1, 4, 1, 64))
+    assert attend_rc(lib, q, kt, v) == L.FFAI_DECLINED
+    q, kt, v = view((1, 4, 512, 64)), view((1, 4, 64, 512)), view((1, 4, 512, 64))
+    assert attend_rc(lib, q, kt, v, masked=1) == L.FFAI_DECLINED
+
+
+@pytest.mark.parametrize("case", ["q_f16", "batch2", "hd128", "short_encoder", "qlen_between",
+                                  "host", "k_f16_v_f32", "heads_mismatch"])
+def test_attend_decline_rules(lib, case):
+    q, kt, v = view((1, 4, 512, 64)), view((1, 4, 64, 512)), view((1, 4, 512, 64))
+    if case == "q_f16":
+        q = view((1, 4, 512, 64), dtype=L.F16)
+    elif case == "batch2":
+        q = view((2, 4, 512, 64))
+    elif case == "hd128":
+        q = view((1, 4, 512, 128))
+    elif case == "short_encoder":  # qlen == keys < MIN_SEQ (256)
+        q, kt, v = view((1, 4, 200, 64)), view((1, 4, 64, 200)), view((1, 4, 200, 64))
+    elif case == "qlen_between":
+        q = view((1, 4, 7, 64))
+    elif case == "host":
+        q = view((1, 4, 512, 64), on_device=0)
+    elif case == "k_f16_v_f32":
+        kt = view((1, 4, 64, 512), dtype=L.F16)
+    elif case == "heads_mismatch":
+        kt = view((1, 3, 64, 512))
+    assert attend_rc(lib, q, kt, v) == L.FFAI_DECLINED
+
+
+def test_attend_errors_match_cpu_fwd_bails(lib):
+    # f16 K/V at the encoder shape passes attend's checks but bails in cpu_fwd
+    # (flash_attn.rs:289-296 then 357-359): an error, not a decline
+    q = view((1, 4, 512, 64))
+    kt, v = view((1, 4, 64, 512), dtype=L.F16), view((1, 4, 512, 64), dtype=L.F16)
+    assert attend_rc(lib, q, kt, v) == L.FFAI_ERR_INVALID
+    # non-contiguous operands bail (flash_attn.rs:360-363)
+    q = view((1, 4, 512, 64), strides=[4 * 512 * 128, 512 * 128, 128, 1])
+    kt, v = view((1, 4, 64, 512)), view((1, 4, 512, 64))
+    assert attend_rc(lib, q, kt, v) == L.FFAI_ERR_INVALID
+
+
+def test_attend_merged_decline_rules(lib):
+    out = view((1, 300, 4 * 64))
+
+    def rc(q, kt, v):
+        return lib.ffai_attend_merged(ctypes.byref(q), ctypes.byref(kt), ctypes.byref(v),
+                                      ctypes.byref(out), None)
+
+    ok = (view((1, 4, 300, 64)), view((1, 4, 64, 300)), view((1, 4, 300, 64)))
+    assert rc(view((1, 4, 300, 64), dtype=L.BF16), ok[1], ok[2]) == L.FFAI_DECLINED
+    assert rc(view((1, 4, 1, 64)), ok[1], ok[2]) == L.FFAI_DECLINED     # qlen != keys
+    short = (view((1, 4, 255, 64)), view((1, 4, 64, 255)), view((1, 4, 255, 64)))
+    assert rc(*short) == L.FFAI_DECLINED                                 # keys < 256
+    assert rc(view((1, 4, 300, 64), on_device=0), ok[1], ok[2]) == L.FFAI_DECLINED
+
+
+def test_serves_tracks_the_decode_floor_knob(lib):
+    """The A1 lesson (flash_attn.rs:113-125): serves must apply the same floor the decode path
+    applies, so raising DECODE_MIN_KEYS above the key count turns serves off."""
+    kt, v = view((1, 16, 64, 1500)), view((1, 16, 1500, 64))
+    saved = lib.ffai_get_decode_min_keys()
+    try:
+        assert lib.ffai_serves(ctypes.byref(kt), ctypes.byref(v)) == 1
+        lib.ffai_set_decode_min_keys(2000)
+        assert lib.ffai_serves(ctypes.byref(kt), ctypes.byref(v)) == 0
+        q = view((1, 16, 1, 64))
+        assert attend_rc(lib, q, kt, v) == L.FFAI_DECLINED  # and the kernel declines too
+    finally:
+        lib.ffai_set_decode_min_keys(saved)
+    short_kt, short_v = view((1, 16, 64, 200)), view((1, 16, 200, 64))
+    assert lib.ffai_serves(ctypes.byref(short_kt), ctypes.byref(short_v)) == 0  # < MIN_SEQ
+    assert lib.ffai_serves(ctypes.byref(view((1, 16, 64, 1500), on_device=0)),
+                           ctypes.byref(v)) == 0
+
+
+def test_python_mirror_declines_host_tensors():
+    import torch
+
+    from ffai_amd import flash_attn as fa
+
+    q = torch.zeros(1, 4, 512, 64)
+    kt = torch.zeros(1, 4, 64, 512)
+    v = torch.zeros(1, 4, 512, 64)
+    assert fa.attend(q, kt, v) is None
+    assert fa.attend_merged(q, kt, v) is None
+    assert fa.serves(kt, v) is False
