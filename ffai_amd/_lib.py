@@ -86,13 +86,15 @@ def load():
     L.ffai_serves.argtypes = [tp, tp]
     L.ffai_attend.argtypes = [tp, tp, tp, ctypes.c_int, tp, vp, sz, vp]
     L.ffai_attend_workspace_bytes.argtypes = [tp, tp, tp, ctypes.POINTER(sz)]
-    L.ffai_attend_merged.argtypes = [tp, tp, tp, tp, vp]
+    L.ffai_attend_merged.argtypes = [tp, tp, tp, tp, vp, sz, vp]
+    L.ffai_attend_merged_workspace_bytes.argtypes = [tp, tp, tp, ctypes.POINTER(sz)]
     L.ffai_get_decode_min_keys.restype = ctypes.c_int
     L.ffai_set_decode_min_keys.argtypes = [ctypes.c_int]
     L.ffai_set_decode_min_keys.restype = None
     L.ffai_attn_last_error.restype = ctypes.c_char_p
     for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
-                 "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged"):
+                 "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
+                 "ffai_attend_merged_workspace_bytes"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

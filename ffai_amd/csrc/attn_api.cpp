@@ -124,7 +124,7 @@ int vec_of(const void* base, size_t esize, const int64_t* strides, int max_vec) 
 }
 
 struct Plan {
-  int waves;
+  int variant;
   int n_qblk;
   int n_split;
   int tiles_per_split;
@@ -132,24 +132,37 @@ struct Plan {
   size_t ws_bytes;
 };
 
-// Launch shape: 4 waves (128 query rows) per workgroup for long queries, 1 wave (32 rows) for
-// short ones; when that still leaves the 256 CUs short of work, split the keys.
+// Launch shape. Long 16-bit head_dim-64 queries: 4 waves x 64 rows per workgroup; other long
+// queries: 4 waves x 32 rows; short ones (decode): 1 wave x 32 rows. A shape that leaves the
+// 256 CUs short of workgroups steps down, then splits the keys: to >= 512 workgroups for the
+// 16-bit kernels, to >= 4096 waves for the f32 kernel, whose long MFMA chains need several
+// waves per SIMD to stay busy.
 Plan make_plan(const ffai_attn_desc* d, bool allow_split) {
   Plan p{};
   const int64_t bh = (int64_t)d->batch * d->heads_q;
+  const bool f32 = d->q_dtype == FFAI_F32;
   const int n_tiles = (d->kv_len + ffai::kBlockN - 1) / ffai::kBlockN;
-  p.waves = d->q_len > 32 ? 4 : 1;
-  int64_t work = bh * ((d->q_len + 32 * p.waves - 1) / (32 * p.waves));
-  if (p.waves == 4 && work < 256) {
-    p.waves = 1;
-    work = bh * ((d->q_len + 31) / 32);
-  }
-  p.n_qblk = (d->q_len + 32 * p.waves - 1) / (32 * p.waves);
+  auto work_of = [&](int v) {
+    const int bm = ffai::block_m_of(v);
+    return bh * ((d->q_len + bm - 1) / bm);
+  };
+  p.variant = ffai::kWave1;
+  if (d->q_len > 32) p.variant = ffai::kWave4;
+  if (!f32 && d->head_dim == 64 && d->q_len >= 256) p.variant = ffai::kWave4x2;
+  if (p.variant == ffai::kWave4x2 && work_of(p.variant) < 256) p.variant = ffai::kWave4;
+  if (p.variant == ffai::kWave4 && work_of(p.variant) < 256) p.variant = ffai::kWave1;
+  const int64_t work = work_of(p.variant);
+  const int bm = ffai::block_m_of(p.variant);
+  p.n_qblk = (d->q_len + bm - 1) / bm;
   p.n_split = 1;
   p.tiles_per_split = n_tiles;
-  if (allow_split && work < 256 && n_tiles >= 2) {
-    const int want = (int)std::min<int64_t>(n_tiles, (512 + work - 1) / work);
-    p.tiles_per_split = (n_tiles + want - 1) / want;
+  const int64_t waves = work * (p.variant == ffai::kWave1 ? 1 : 4);
+  int64_t want = 1;
+  if (f32) want = (4096 + waves - 1) / waves;
+  else if (work < 256) want = (512 + work - 1) / work;
+  if (allow_split && want > 1 && n_tiles >= 2) {
+    want = std::min<int64_t>(want, n_tiles);
+    p.tiles_per_split = (int)((n_tiles + want - 1) / want);
     p.n_split = (n_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
   }
   p.n_work = (int)(work * p.n_split);
@@ -190,26 +203,28 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   p.causal = d->causal; p.q_offset = d->q_offset;
   p.n_qblk = pl.n_qblk; p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split;
   p.n_work = pl.n_work;
-  const int qmax = d->q_dtype == FFAI_F32 ? 4 : 8;
-  const int kmax = d->q_dtype == FFAI_F32 ? 4 : 8;  // f32 kernel stages K/V four at a time
-  p.q_vec = vec_of(q, qs, d->q_strides, qmax);
-  p.k_vec = vec_of(k, ks, d->k_strides, kmax);
-  p.v_vec = vec_of(v, ks, d->v_strides, kmax);
-  p.o_vec = vec_of(out, os, d->o_strides, 4);
+  // The kernels' vector accesses: Q rows 16 B (4 f32 or 8 16-bit elements); K rows and V rows
+  // 16 B in the 16-bit kernels, 4 elements in the f32 kernel; K^T rows 4 keys; O 4 elements.
+  const bool f32 = d->q_dtype == FFAI_F32;
+  const bool kt = d->k_layout == FFAI_K_TRANSPOSED;
+  const int need_q = f32 ? 4 : 8, need_kv = f32 ? 4 : 8, need_k = kt ? 4 : need_kv;
+  p.aligned = vec_of(q, qs, d->q_strides, need_q) == need_q &&
+              vec_of(k, ks, d->k_strides, need_k) == need_k &&
+              vec_of(v, ks, d->v_strides, need_kv) == need_kv &&
+              vec_of(out, os, d->o_strides, 4) == 4;
   p.scale_log2 = d->scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int mode = d->q_dtype == FFAI_F32 ? ffai::kF32 : (d->q_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
   const int kvt = d->kv_dtype == FFAI_F32 ? ffai::kF32 : (d->kv_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
   const int ot = d->out_dtype == FFAI_F32 ? ffai::kF32 : (d->out_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
-  hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, d->k_layout == FFAI_K_TRANSPOSED,
-                                  pl.waves, s);
+  hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt, pl.variant, s);
   if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));
   if (pl.n_split > 1) {
     ffai::CombineParams c{};
     c.ws = p.ws; c.o = out;
     c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
-    c.B = p.B; c.Hq = p.Hq; c.Tq = p.Tq; c.n_split = p.n_split; c.scale_log2 = p.scale_log2;
+    c.B = p.B; c.Hq = p.Hq; c.Tq = p.Tq; c.n_split = p.n_split;
     e = ffai::launch_combine(c, ot, d->head_dim, s);
     if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("combine launch: ") + hipGetErrorString(e));
   }
@@ -261,6 +276,35 @@ void attend_desc(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor*
   ffai_attn_desc_init(d, FFAI_F32, kt->dtype, FFAI_F32, 1, heads, heads, qlen, keys, kHD,
                       FFAI_K_TRANSPOSED);
   (void)v;
+}
+
+// attend_merged's accept set (flash_attn.rs:135-153).
+int merged_accepts(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
+                   std::string* why) {
+  const int64_t b = q->dims[0], heads = q->dims[1], qlen = q->dims[2], hd = q->dims[3];
+  if (b != 1 || hd != kHD || !q->on_device || !kt->on_device || !v->on_device) {
+    *why = "batch 1, head_dim 64, device tensors only"; return FFAI_DECLINED;
+  }
+  if (q->dtype != FFAI_F32 || kt->dtype != FFAI_F32 || v->dtype != FFAI_F32) {
+    *why = "f32 only"; return FFAI_DECLINED;
+  }
+  if (kt->dims[0] != 1 || kt->dims[1] != heads || kt->dims[2] != kHD) { *why = "kt shape"; return FFAI_DECLINED; }
+  const int64_t keys = kt->dims[3];
+  if (!dims_are(v, 1, heads, keys, kHD) || qlen != keys || keys < kMinSeq) {
+    *why = "v shape, qlen != keys or keys < 256"; return FFAI_DECLINED;
+  }
+  return FFAI_OK;
+}
+
+// Merged layout: query row i of head h lands at i*H*64 + h*64 (flash_attn.rs:188-207).
+void merged_desc(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
+                 ffai_attn_desc* d) {
+  attend_desc(q, kt, v, d);
+  const int64_t heads = q->dims[1], keys = kt->dims[3];
+  d->o_strides[0] = keys * heads * kHD;
+  d->o_strides[1] = kHD;
+  d->o_strides[2] = heads * kHD;
+  d->o_strides[3] = 1;
 }
 
 }  // namespace
@@ -348,33 +392,34 @@ int ffai_attend(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* 
 }
 
 int ffai_attend_merged(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
-                       ffai_tensor* out, void* stream) {
+                       ffai_tensor* out, void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error.clear();
   if (!q || !kt || !v || !out) return fail(FFAI_ERR_INVALID, "null tensor");
-  // attend_merged's accept set (flash_attn.rs:135-153)
-  const int64_t b = q->dims[0], heads = q->dims[1], qlen = q->dims[2], hd = q->dims[3];
-  if (b != 1 || hd != kHD || !q->on_device || !kt->on_device || !v->on_device)
-    return fail(FFAI_DECLINED, "declined: batch 1, head_dim 64, device tensors only");
-  if (q->dtype != FFAI_F32 || kt->dtype != FFAI_F32 || v->dtype != FFAI_F32)
-    return fail(FFAI_DECLINED, "declined: f32 only");
-  if (kt->dims[0] != 1 || kt->dims[1] != heads || kt->dims[2] != kHD)
-    return fail(FFAI_DECLINED, "declined: kt shape");
-  const int64_t keys = kt->dims[3];
-  if (!dims_are(v, 1, heads, keys, kHD) || qlen != keys || keys < kMinSeq)
-    return fail(FFAI_DECLINED, "declined: v shape, qlen != keys or keys < 256");
+  std::string why;
+  if (merged_accepts(q, kt, v, &why) != FFAI_OK) return fail(FFAI_DECLINED, "declined: " + why);
+  const int64_t heads = q->dims[1], keys = kt->dims[3];
   if (!contiguous(q) || !contiguous(kt) || !contiguous(v))
     return fail(FFAI_ERR_INVALID, "flash-attn-merged: contiguous only");
   if (out->dtype != FFAI_F32 || !out->on_device || !dims_are(out, 1, keys, heads * kHD, 1) ||
       out->strides[0] != keys * heads * kHD || out->strides[1] != heads * kHD || out->strides[2] != 1)
     return fail(FFAI_ERR_INVALID, "out must be a contiguous f32 (1,T,H*64) device tensor");
   ffai_attn_desc d;
-  attend_desc(q, kt, v, &d);
-  // merged layout: row i of head h at i*H*64 + h*64
-  d.o_strides[0] = keys * heads * kHD;
-  d.o_strides[1] = kHD;
-  d.o_strides[2] = heads * kHD;
-  d.o_strides[3] = 1;
-  return run_fwd(&d, q->data, kt->data, v->data, out->data, nullptr, 0, stream, false);
+  merged_desc(q, kt, v, &d);
+  return run_fwd(&d, q->data, kt->data, v->data, out->data, workspace, workspace_bytes, stream,
+                 true);
+}
+
+int ffai_attend_merged_workspace_bytes(const ffai_tensor* q, const ffai_tensor* kt,
+                                       const ffai_tensor* v, size_t* bytes) {
+  if (!bytes) return fail(FFAI_ERR_INVALID, "null bytes pointer");
+  *bytes = 0;
+  if (!q || !kt || !v) return fail(FFAI_ERR_INVALID, "null tensor");
+  std::string why;
+  if (merged_accepts(q, kt, v, &why) != FFAI_OK) return fail(FFAI_DECLINED, "declined: " + why);
+  ffai_attn_desc d;
+  merged_desc(q, kt, v, &d);
+  *bytes = make_plan(&d, true).ws_bytes;
+  return FFAI_OK;
 }
 
 int ffai_get_decode_min_keys(void) { return decode_min_keys(); }

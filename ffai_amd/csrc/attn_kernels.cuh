@@ -1,26 +1,29 @@
 // gfx950 (MI355X) fused attention kernels: O = softmax(scale * Q K^T [+ mask]) V in one pass.
 //
-// Design (one workgroup = NW waves = 32*NW query rows of one (batch, q-head); keys in tiles
-// of 64):
+// Design (one workgroup = NW waves; each wave owns QW x 32 query rows of one (batch, q-head);
+// keys stream in tiles of 64):
 //   * Both contractions run on MFMA with the score tile computed TRANSPOSED, S^T = K Q^T
 //     (32 keys x 32 queries per v_mfma_f32_32x32x16_{bf16,f16} / 32x32x2_f32). In the 32x32
 //     accumulator layout lane l owns query column l%32 and 16 of the 32 keys, lane l^32 the
 //     other 16, so every softmax statistic (row max, row sum, rescale factor) is a per-lane
-//     scalar: the only cross-lane traffic is one exchange with lane l^32 per tile for the max.
+//     scalar; the only cross-lane step is one v_permlane32_swap per tile for the row max.
 //   * The probabilities stay in registers: the accumulator of S^T is already the B operand
 //     of O^T = V^T P^T once the key order inside each 16-key MFMA step is permuted the same
 //     way on both operands (the contraction is a sum, so any shared order is exact).
-//   * K and V tiles are staged through LDS once per workgroup: K as rows [key][d] (A operand
-//     of the first product), V transposed [d][key] (A operand of the second). The reference's
-//     K^T layout and V's row layout are transposed on the way in with register permutes.
-//     The next tile's global loads are issued before the current tile's MFMAs.
-//   * Online softmax in base 2: p = exp2(s*scale*log2e - m*scale*log2e) with v_exp_f32; the
-//     accumulator is rescaled by exp2(m_old - m_new) per tile.
+//   * With QW = 2 a wave computes two 32-query column blocks against each K/V fragment it
+//     reads from LDS, halving LDS operand traffic per FLOP (at 32 queries per wave the LDS
+//     read bandwidth alone would cap the MFMA pipes near 80 %).
+//   * K and V tiles are staged through double-buffered LDS once per workgroup: K as rows
+//     [key][d] (A operand of the first product), V transposed [d][key] (A operand of the
+//     second). The reference's K^T layout and V's row layout are transposed on the way in with
+//     register permutes. Global loads run two tiles ahead; one barrier per tile.
+//   * Online softmax in base 2 with v_exp_f32. The running max only moves when a tile's max
+//     exceeds it by more than 2^8 in probability (the weights then stay below 256, exact in f32
+//     and bf16 alike), so after the first tile the accumulator rescale is almost never paid.
 //   * Workgroup ids are remapped so that all query blocks of one (batch, kv-head) run on the
 //     same XCD (the hardware deals workgroup i to XCD i % 8) and share that XCD's L2.
 //   * Few-query shapes (decode) split the keys over workgroups; partial (O, m, l) go to the
 //     workspace and combine_kernel merges them by log-sum-exp.
-
 #pragma once
 
 #include "attn_kernels.h"
@@ -36,16 +39,20 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BN = kBlockN;
 constexpr float kNegInf = -__builtin_huge_valf();
+// The running max is only raised when a tile's max exceeds it by more than this (log2 units).
+constexpr float kRescaleSlack = 8.0f;
 
 template <int DT>
 using store_t = std::conditional_t<DT == kF32, float, uint16_t>;
 
 // ---------------------------------------------------------------------------------------------
-// Scalar conversions.
+// Conversions.
 // ---------------------------------------------------------------------------------------------
 template <int DT>
 __device__ __forceinline__ float to_f32(uint32_t bits16) {
@@ -56,111 +63,56 @@ __device__ __forceinline__ float to_f32(uint32_t bits16) {
   }
 }
 
+// Two floats to a packed pair (round to nearest even; one v_cvt_pk_* instruction).
 template <int DT>
-__device__ __forceinline__ uint32_t from_f32(float x) {  // round to nearest even
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2 x = {lo, hi};
   if constexpr (DT == kBF16) {
-    return __builtin_bit_cast(uint16_t, (__bf16)x);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
   } else {
-    return __builtin_bit_cast(uint16_t, (_Float16)x);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
   }
 }
 
 template <int DT>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return from_f32<DT>(lo) | (from_f32<DT>(hi) << 16);
+__device__ __forceinline__ uint16_t from_f32(float x) {
+  return (uint16_t)(pack2<DT>(x, 0.f) & 0xffffu);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// ---------------------------------------------------------------------------------------------
-// Global loads of short contiguous runs. `n` elements are valid (the rest read as zero and are
-// never touched); `vec` is the widest access, in elements, that every address of this operand is
-// aligned to (uniform over the launch).
-// ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ u32x4 load8_h(const uint16_t* p, int n, int vec) {
-  if (n >= 8) {
-    if (vec >= 8) return *reinterpret_cast<const u32x4*>(p);
-    if (vec >= 4) {
-      const u32x2 a = reinterpret_cast<const u32x2*>(p)[0];
-      const u32x2 b = reinterpret_cast<const u32x2*>(p)[1];
-      return u32x4{a.x, a.y, b.x, b.y};
-    }
-    if (vec >= 2) {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
-      return u32x4{w[0], w[1], w[2], w[3]};
-    }
-  }
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    if (e < n) w[e >> 1] |= (uint32_t)p[e] << (16 * (e & 1));
-  return u32x4{w[0], w[1], w[2], w[3]};
+// The same value from lane l and lane l^32 (v_permlane32_swap): returns {own, partner} in some
+// order, which is all a max or a sum needs.
+__device__ __forceinline__ float partner_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-
-// Four elements widened to f32 (source f32, f16 or bf16).
-template <int DT>
-__device__ __forceinline__ f32x4 load4_f(const store_t<DT>* p, int n, int vec) {
-  if constexpr (DT == kF32) {
-    if (n >= 4) {
-      if (vec >= 4) return *reinterpret_cast<const f32x4*>(p);
-      if (vec >= 2) {
-        const f32x2 a = reinterpret_cast<const f32x2*>(p)[0];
-        const f32x2 b = reinterpret_cast<const f32x2*>(p)[1];
-        return f32x4{a.x, a.y, b.x, b.y};
-      }
-    }
-    f32x4 r = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (e < n) r[e] = p[e];
-    return r;
-  } else {
-    uint32_t w0 = 0u, w1 = 0u;
-    if (n >= 4 && vec >= 4) {
-      const u32x2 a = *reinterpret_cast<const u32x2*>(p);
-      w0 = a.x;
-      w1 = a.y;
-    } else if (n >= 4 && vec >= 2) {
-      w0 = reinterpret_cast<const uint32_t*>(p)[0];
-      w1 = reinterpret_cast<const uint32_t*>(p)[1];
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (e < n) {
-          const uint32_t x = (uint32_t)p[e] << (16 * (e & 1));
-          if (e < 2) w0 |= x; else w1 |= x;
-        }
-    }
-    return f32x4{to_f32<DT>(w0 & 0xffffu), to_f32<DT>(w0 >> 16), to_f32<DT>(w1 & 0xffffu),
-                 to_f32<DT>(w1 >> 16)};
-  }
-}
-
-// Store four consecutive outputs.
-template <int DT>
-__device__ __forceinline__ void store4(store_t<DT>* p, f32x4 x, int vec) {
-  if constexpr (DT == kF32) {
-    if (vec >= 4) {
-      *reinterpret_cast<f32x4*>(p) = x;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = x[e];
-    }
-  } else {
-    if (vec >= 4) {
-      *reinterpret_cast<u32x2*>(p) = u32x2{pack2<DT>(x[0], x[1]), pack2<DT>(x[2], x[3])};
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = (uint16_t)from_f32<DT>(x[e]);
-    }
-  }
+__device__ __forceinline__ float partner_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Element k (0..7) of eight 16-bit values held in a u32x4, paired with the same element of a
 // second row: low half from `r0`, high half from `r1` (one v_perm_b32).
 __device__ __forceinline__ uint32_t pair_elem(u32x4 r0, u32x4 r1, int k) {
   const uint32_t a = r0[k >> 1], b = r1[k >> 1];
-  return (k & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
+  return (k & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
+                 : __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+// Same for four 16-bit values held in a u32x2.
+__device__ __forceinline__ uint32_t pair_elem4(u32x2 r0, u32x2 r1, int k) {
+  const uint32_t a = r0[k >> 1], b = r1[k >> 1];
+  return (k & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
+                 : __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16): see the geometry note at its use.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_tr(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4* lds_ptr;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p)));
 }
 
 template <int DT>
@@ -179,24 +131,94 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Loads. "vec" loads assume the launch's alignment check passed; "elem" loads take any address.
+// Every helper reads only addresses of valid elements: callers clamp indices into range and
+// zero what is out of range, so no branch (and no wait) splits a tile's loads.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
+
+// 8 consecutive 16-bit elements, element-wise (any alignment).
+__device__ __forceinline__ u32x4 ld8h_elem(const uint16_t* p) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Four elements widened to f32 from f32, f16 or bf16 storage.
+template <int DT, bool VEC>
+__device__ __forceinline__ f32x4 ld4f(const store_t<DT>* p) {
+  if constexpr (DT == kF32) {
+    if constexpr (VEC) return *reinterpret_cast<const f32x4*>(p);
+    return f32x4{p[0], p[1], p[2], p[3]};
+  } else {
+    uint32_t w0, w1;
+    if constexpr (VEC) {
+      const u32x2 a = ld8(p);
+      w0 = a.x;
+      w1 = a.y;
+    } else {
+      w0 = (uint32_t)p[0] | ((uint32_t)p[1] << 16);
+      w1 = (uint32_t)p[2] | ((uint32_t)p[3] << 16);
+    }
+    return f32x4{to_f32<DT>(w0 & 0xffffu), to_f32<DT>(w0 >> 16), to_f32<DT>(w1 & 0xffffu),
+                 to_f32<DT>(w1 >> 16)};
+  }
+}
+
+// Store four consecutive outputs.
+template <int DT, bool VEC>
+__device__ __forceinline__ void st4(store_t<DT>* p, f32x4 x) {
+  if constexpr (DT == kF32) {
+    if constexpr (VEC) {
+      *reinterpret_cast<f32x4*>(p) = x;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[e] = x[e];
+    }
+  } else {
+    const uint32_t a = pack2<DT>(x[0], x[1]), b = pack2<DT>(x[2], x[3]);
+    if constexpr (VEC) {
+      *reinterpret_cast<u32x2*>(p) = u32x2{a, b};
+    } else {
+      p[0] = (uint16_t)(a & 0xffffu);
+      p[1] = (uint16_t)(a >> 16);
+      p[2] = (uint16_t)(b & 0xffffu);
+      p[3] = (uint16_t)(b >> 16);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // The forward kernel.
 //   MODE  kBF16 / kF16: Q, K, V are that 16-bit type; both products on 32x32x16 MFMA.
 //         kF32: Q f32, K/V of type KVT widened to f32 in LDS; both products on 32x32x2 f32 MFMA.
 //   OUTT  output type. D head_dim. KT: K given transposed (d-major). NW waves per workgroup.
+//   QW    32-query column blocks per wave.
 // ---------------------------------------------------------------------------------------------
-template <int MODE, int KVT, int OUTT, int D, bool KT, int NW>
-__global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
+template <int MODE, int KVT, int OUTT, int D, bool KT, int NW, int QW>
+__global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_kernel(FwdParams p) {
   constexpr int NT = NW * 64;
   constexpr bool F32 = (MODE == kF32);
   using LT = std::conditional_t<F32, float, uint16_t>;  // LDS / compute storage type
   using KVS = store_t<KVT>;                            // K/V global storage type
   using QS = store_t<MODE>;                            // Q global storage type
   static_assert(F32 || KVT == MODE, "16-bit kernels read Q, K and V of one type");
-  // LDS rows padded so that the MFMA operand reads below are bank-conflict free.
-  constexpr int KROW = F32 ? D + 4 : D + 8;   // K rows [key][d]
-  constexpr int VROW = BN + 4;                // V^T rows [d][key]
-  __shared__ __attribute__((aligned(16))) LT k_lds[BN * KROW];
-  __shared__ __attribute__((aligned(16))) LT v_lds[D * VROW];
+  static_assert(!F32 || QW == 1, "the f32 kernel uses one column block per wave");
+  // LDS tiles, rows padded so that the 128-bit stores and the MFMA operand reads are
+  // bank-conflict free.
+  //   f32:    K [key][d] (KROW = D + 4), V^T [d][key] (VROW = BN + 4) - transposed on the way in.
+  //   16-bit: K [key][d] (KROW = D + 8) when K comes as rows, K^T [d][key] (KTROW = BN + 16) when
+  //           it comes transposed, V [key][d] (VROW = D + 16): all stored as they come, and the
+  //           operands that need the other orientation are read with ds_read_b64_tr_b16.
+  constexpr int KROW = F32 ? D + 4 : D + 8;
+  constexpr int KTROW = BN + 16;
+  constexpr int VROW = F32 ? BN + 4 : D + 16;
+  constexpr int KBUF = (!F32 && KT) ? D * KTROW : BN * KROW;
+  constexpr int VBUF = F32 ? D * VROW : BN * VROW;
+  __shared__ __attribute__((aligned(16))) LT k_lds[2 * KBUF];
+  __shared__ __attribute__((aligned(16))) LT v_lds[2 * VBUF];
 
   // ---- which (batch, head, query block, key split) this workgroup computes
   const int hw = blockIdx.x;
@@ -217,9 +239,8 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   const int wave = tid >> 6;
   const int g = lane >> 5;    // lane group: which half of each MFMA contraction step
   const int n32 = lane & 31;  // query column of the accumulators
-  constexpr int BM = NW * 32;
-  const int q0 = qb * BM + wave * 32;  // this wave's first query row
-  const int qrow = q0 + n32;
+  constexpr int BM = NW * 32 * QW;
+  const int q0 = qb * BM + wave * 32 * QW;  // this wave's first query row
 
   int kv_end = p.Tk;
   if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
@@ -228,6 +249,7 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
   const int n_tiles = (kv_blk + BN - 1) / BN;
   const int t_begin = split * p.tiles_per_split;
   const int t_end = min(n_tiles, t_begin + p.tiles_per_split);
+  const bool aligned = p.aligned != 0;
 
   const QS* qp = reinterpret_cast<const QS*>(p.q) + b * p.q_sb + h * p.q_sh;
   const KVS* kp = reinterpret_cast<const KVS*>(p.k) + b * p.k_sb + hk * p.k_sh;
@@ -235,100 +257,141 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole key loop
   constexpr int QF = F32 ? D / 2 : D / 16;
-  std::conditional_t<F32, float, u32x4> qf[QF];
-  {
-    const bool ok = qrow < p.Tq;
-    const QS* qr = qp + (int64_t)qrow * p.q_st;
+  std::conditional_t<F32, float, u32x4> qf[QW][QF];
+#pragma unroll
+  for (int c = 0; c < QW; ++c) {
+    const int row = q0 + 32 * c + n32;
+    const bool ok = row < p.Tq;
+    const QS* qr = qp + (int64_t)min(row, p.Tq - 1) * p.q_st;
     if constexpr (F32) {
       // step (j, e): lane group g supplies d = 8j + 4g + e
 #pragma unroll
       for (int j = 0; j < D / 8; ++j) {
-        const f32x4 x = load4_f<kF32>(qr + 8 * j + 4 * g, ok ? 4 : 0, p.q_vec);
+        const f32x4 x = aligned ? ld4f<kF32, true>(qr + 8 * j + 4 * g)
+                                : ld4f<kF32, false>(qr + 8 * j + 4 * g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) qf[4 * j + e] = x[e];
+        for (int e = 0; e < 4; ++e) qf[c][4 * j + e] = ok ? x[e] : 0.f;
       }
     } else {
       // step s: lane group g supplies d = 16s + 8g .. +7
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) qf[s] = load8_h(qr + 16 * s + 8 * g, ok ? 8 : 0, p.q_vec);
+      for (int s = 0; s < D / 16; ++s) {
+        const u32x4 x = aligned ? ld16(qr + 16 * s + 8 * g) : ld8h_elem(qr + 16 * s + 8 * g);
+        qf[c][s] = ok ? x : u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
 
-  // ---- staging registers for one K/V tile
-  // 16-bit: K rows -> units of 8 elements; K^T -> units of (2 d-rows x 8 keys); V -> units of
-  //         (2 keys x 8 d). f32: K rows -> 4 elements; K^T -> (4 d-rows x 4 keys); V -> (4 x 4).
+  // ---- staging: global -> registers (two tiles ahead) -> LDS
+  // f32:    K rows -> units of 4 elements; K^T -> 4 d-rows x 4 keys (transposed in registers);
+  //         V -> 4 keys x 4 d (transposed in registers).
+  // 16-bit: K rows, K^T rows and V rows -> units of 8 elements (one 128-bit LDS store each);
+  //         K^T rows are only 8-byte aligned in general (row stride = key count), so they are
+  //         read from global memory as two 8-byte halves.
   constexpr int K_UNITS = F32 ? (KT ? (D / 4) * (BN / 4) : BN * (D / 4))
-                              : (KT ? (D / 2) * (BN / 8) : BN * (D / 8));
-  constexpr int V_UNITS = F32 ? (BN / 4) * (D / 4) : (BN / 2) * (D / 8);
-  constexpr int K_PER = (K_UNITS + NT - 1) / NT;
-  constexpr int V_PER = (V_UNITS + NT - 1) / NT;
-  constexpr int K_REGS = F32 ? (KT ? 4 : 1) : (KT ? 2 : 1);  // loads per unit
-  constexpr int V_REGS = F32 ? 4 : 2;
+                              : (KT ? D * (BN / 8) : BN * (D / 8));
+  constexpr int V_UNITS = F32 ? (BN / 4) * (D / 4) : BN * (D / 8);
+  static_assert(K_UNITS % NT == 0 && V_UNITS % NT == 0, "staging units must tile the workgroup");
+  constexpr int K_PER = K_UNITS / NT;
+  constexpr int V_PER = V_UNITS / NT;
   using SR = std::conditional_t<F32, f32x4, u32x4>;
+  constexpr int K_REGS = F32 ? (KT ? 4 : 1) : 1;  // registers per unit
+  constexpr int V_REGS = F32 ? 4 : 1;
   SR kreg[K_PER * K_REGS];
   SR vreg[V_PER * V_REGS];
 
+  // Load tile `it` into kreg/vreg. Interior tiles of an aligned launch take unconditional
+  // vector loads (the uniform `full` branch); tail tiles clamp every index to the last valid key
+  // and zero what lies past it, so they too read only valid addresses without divergent branches.
   auto load_tile = [&](int it) {
     const int kb = it * BN;
+    const int klast = kv_end - 1;
+    const bool full = aligned && (kb + BN <= kv_end);
 #pragma unroll
     for (int i = 0; i < K_PER; ++i) {
       const int u = tid + i * NT;
-      if (K_UNITS % NT != 0 && u >= K_UNITS) continue;
       if constexpr (F32) {
         if constexpr (KT) {
           const int d4 = u / (BN / 4), k4 = u % (BN / 4);
           const int key0 = kb + 4 * k4;
-          const int n = min(max(kv_end - key0, 0), 4);
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            kreg[4 * i + r] = load4_f<KVT>(kp + (int64_t)(4 * d4 + r) * p.k_st + key0, n, p.k_vec);
+          for (int r = 0; r < 4; ++r) {
+            const KVS* row = kp + (int64_t)(4 * d4 + r) * p.k_st;
+            f32x4 x;
+            if (full) {
+              x = ld4f<KVT, true>(row + key0);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const KVS y = row[min(key0 + e, klast)];
+                float f;
+                if constexpr (KVT == kF32) f = y;
+                else f = to_f32<KVT>(y);
+                x[e] = (key0 + e <= klast) ? f : 0.f;
+              }
+            }
+            kreg[4 * i + r] = x;
+          }
         } else {
-          const int key = u / (D / 4), c = u % (D / 4);
-          const int ok = (kb + key < kv_end) ? 4 : 0;
-          kreg[i] = load4_f<KVT>(kp + (int64_t)(kb + key) * p.k_st + 4 * c, ok, p.k_vec);
+          const int key = kb + u / (D / 4), c = u % (D / 4);
+          const KVS* src = kp + (int64_t)min(key, klast) * p.k_st + 4 * c;
+          const f32x4 x = aligned ? ld4f<KVT, true>(src) : ld4f<KVT, false>(src);
+          kreg[i] = (full || key <= klast) ? x : f32x4{0.f, 0.f, 0.f, 0.f};
         }
       } else {
         if constexpr (KT) {
-          const int dp = u / (BN / 8), kc = u % (BN / 8);
+          const int d = u / (BN / 8), kc = u % (BN / 8);
           const int key0 = kb + 8 * kc;
-          const int n = min(max(kv_end - key0, 0), 8);
-          const KVS* r0 = kp + (int64_t)(2 * dp) * p.k_st + key0;
-          kreg[2 * i] = load8_h(r0, n, p.k_vec);
-          kreg[2 * i + 1] = load8_h(r0 + p.k_st, n, p.k_vec);
+          const uint16_t* row = kp + (int64_t)d * p.k_st;
+          u32x4 x;
+          if (full) {
+            const u32x2 lo = ld8(row + key0), hi = ld8(row + key0 + 4);
+            x = u32x4{lo.x, lo.y, hi.x, hi.y};
+          } else {
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const uint32_t y = row[min(key0 + e, klast)];
+              w[e >> 1] |= (key0 + e <= klast ? y : 0u) << (16 * (e & 1));
+            }
+            x = u32x4{w[0], w[1], w[2], w[3]};
+          }
+          kreg[i] = x;
         } else {
-          const int key = u / (D / 8), c = u % (D / 8);
-          const int ok = (kb + key < kv_end) ? 8 : 0;
-          kreg[i] = load8_h(kp + (int64_t)(kb + key) * p.k_st + 8 * c, ok, p.k_vec);
+          const int key = kb + u / (D / 8), c = u % (D / 8);
+          const uint16_t* src = kp + (int64_t)min(key, klast) * p.k_st + 8 * c;
+          const u32x4 x = aligned ? ld16(src) : ld8h_elem(src);
+          kreg[i] = (full || key <= klast) ? x : u32x4{0u, 0u, 0u, 0u};
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < V_PER; ++i) {
       const int u = tid + i * NT;
-      if (V_UNITS % NT != 0 && u >= V_UNITS) continue;
       if constexpr (F32) {
         const int k4 = u / (D / 4), d4 = u % (D / 4);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = kb + 4 * k4 + r;
-          vreg[4 * i + r] =
-              load4_f<KVT>(vp + (int64_t)key * p.v_st + 4 * d4, key < kv_end ? 4 : 0, p.v_vec);
+          const KVS* src = vp + (int64_t)min(key, klast) * p.v_st + 4 * d4;
+          const f32x4 x = aligned ? ld4f<KVT, true>(src) : ld4f<KVT, false>(src);
+          vreg[4 * i + r] = (full || key <= klast) ? x : f32x4{0.f, 0.f, 0.f, 0.f};
         }
       } else {
-        const int kp2 = u / (D / 8), c = u % (D / 8);
-        const int key = kb + 2 * kp2;
-        vreg[2 * i] = load8_h(vp + (int64_t)key * p.v_st + 8 * c, key < kv_end ? 8 : 0, p.v_vec);
-        vreg[2 * i + 1] =
-            load8_h(vp + (int64_t)(key + 1) * p.v_st + 8 * c, key + 1 < kv_end ? 8 : 0, p.v_vec);
+        const int key = kb + u / (D / 8), c = u % (D / 8);
+        const uint16_t* src = vp + (int64_t)min(key, klast) * p.v_st + 8 * c;
+        const u32x4 x = aligned ? ld16(src) : ld8h_elem(src);
+        vreg[i] = (full || key <= klast) ? x : u32x4{0u, 0u, 0u, 0u};
       }
     }
   };
 
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
+    LT* kl = k_lds + buf * KBUF;
+    LT* vl = v_lds + buf * VBUF;
 #pragma unroll
     for (int i = 0; i < K_PER; ++i) {
       const int u = tid + i * NT;
-      if (K_UNITS % NT != 0 && u >= K_UNITS) continue;
       if constexpr (F32) {
         if constexpr (KT) {
           const int d4 = u / (BN / 4), k4 = u % (BN / 4);
@@ -336,133 +399,131 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
           for (int c = 0; c < 4; ++c) {
             const f32x4 col = {kreg[4 * i][c], kreg[4 * i + 1][c], kreg[4 * i + 2][c],
                                kreg[4 * i + 3][c]};
-            *reinterpret_cast<f32x4*>(&k_lds[(4 * k4 + c) * KROW + 4 * d4]) = col;
+            *reinterpret_cast<f32x4*>(&kl[(4 * k4 + c) * KROW + 4 * d4]) = col;
           }
         } else {
           const int key = u / (D / 4), c = u % (D / 4);
-          *reinterpret_cast<f32x4*>(&k_lds[key * KROW + 4 * c]) = kreg[i];
+          *reinterpret_cast<f32x4*>(&kl[key * KROW + 4 * c]) = kreg[i];
         }
       } else {
         if constexpr (KT) {
-          const int dp = u / (BN / 8), kc = u % (BN / 8);
-          uint32_t* kw = reinterpret_cast<uint32_t*>(k_lds);
-#pragma unroll
-          for (int kk = 0; kk < 8; ++kk)
-            kw[(8 * kc + kk) * (KROW / 2) + dp] = pair_elem(kreg[2 * i], kreg[2 * i + 1], kk);
+          const int d = u / (BN / 8), kc = u % (BN / 8);
+          *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * kc]) = kreg[i];
         } else {
           const int key = u / (D / 8), c = u % (D / 8);
-          *reinterpret_cast<u32x4*>(&k_lds[key * KROW + 8 * c]) = kreg[i];
+          *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * c]) = kreg[i];
         }
       }
     }
 #pragma unroll
     for (int i = 0; i < V_PER; ++i) {
       const int u = tid + i * NT;
-      if (V_UNITS % NT != 0 && u >= V_UNITS) continue;
       if constexpr (F32) {
         const int k4 = u / (D / 4), d4 = u % (D / 4);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const f32x4 col = {vreg[4 * i][c], vreg[4 * i + 1][c], vreg[4 * i + 2][c],
                              vreg[4 * i + 3][c]};
-          *reinterpret_cast<f32x4*>(&v_lds[(4 * d4 + c) * VROW + 4 * k4]) = col;
+          *reinterpret_cast<f32x4*>(&vl[(4 * d4 + c) * VROW + 4 * k4]) = col;
         }
       } else {
-        const int kp2 = u / (D / 8), c = u % (D / 8);
-        uint32_t* vw = reinterpret_cast<uint32_t*>(v_lds);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          vw[(8 * c + e) * (VROW / 2) + kp2] = pair_elem(vreg[2 * i], vreg[2 * i + 1], e);
+        const int key = u / (D / 8), c = u % (D / 8);
+        *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * c]) = vreg[i];
       }
     }
   };
 
-  // ---- online-softmax state: this lane's query row, its half of the keys
-  f32x16 oacc[D / 32];
+  // ---- online-softmax state, per column block: this lane's query row, its half of the keys
+  f32x16 oacc[QW][D / 32];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int c = 0; c < QW; ++c)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  float m_run = kNegInf;  // running max of raw scores (row-wide after the exchange)
-  float l_run = 0.f;      // running sum of this lane's weights
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[c][dt][r] = 0.f;
+  float m_s[QW];  // running max, already multiplied by scale*log2(e) (row-wide)
+  float l_run[QW];  // running sum of this lane's weights
+#pragma unroll
+  for (int c = 0; c < QW; ++c) {
+    m_s[c] = kNegInf;
+    l_run[c] = 0.f;
+  }
   const float sl2 = p.scale_log2;
 
-  if (t_begin < t_end) load_tile(t_begin);
-  for (int it = t_begin; it < t_end; ++it) {
-    __syncthreads();  // every wave is done reading the previous tile
-    store_tile();
-    __syncthreads();
-    if (it + 1 < t_end) load_tile(it + 1);  // in flight during this tile's MFMAs
+  if (t_begin < t_end) {
+    load_tile(t_begin);
+    store_tile(0);
+    if (t_begin + 1 < t_end) load_tile(t_begin + 1);
+  }
+  __syncthreads();
 
-    // ---- S^T = K Q^T for 2 x 32 keys: sacc[st][i] <-> key 32st + 8(i/4) + 4g + i%4
-    f32x16 sacc[2];
+  // Mask the keys of 32-key subtile `st` past each row's end (ragged tail, causal diagonal).
+  // sacc[c][st][i] <-> key kb + 32st + 8(i/4) + 4g + i%4 of query q0 + 32c + n32.
+  auto mask_subtile = [&](f32x16 (&sacc)[QW][2], int kb, int st) {
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int c = 0; c < QW; ++c) {
+      const int qrow = q0 + 32 * c + n32;
+      const int lim = p.causal ? min(kv_end - 1, p.q_offset + qrow) : kv_end - 1;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[st][r] = 0.f;
-    if constexpr (F32) {
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + 32 * st + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key > lim) sacc[c][st][r] = kNegInf;
+      }
+    }
+  };
+
+  if constexpr (F32) {
+    // ---------------------------------------------------------------------------------------
+    // f32: both products on 32x32x2 f32 MFMA (MFMA-bound by a wide margin; no interleaving).
+    // ---------------------------------------------------------------------------------------
+    for (int it = t_begin; it < t_end; ++it) {
+      const int buf = (it - t_begin) & 1;
+      const LT* kl = k_lds + buf * KBUF;
+      const LT* vl = v_lds + buf * VBUF;
+      f32x16 sacc[QW][2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[0][st][r] = 0.f;
 #pragma unroll
       for (int j = 0; j < D / 8; ++j)
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
           const f32x4 a =
-              *reinterpret_cast<const f32x4*>(&k_lds[(32 * st + n32) * KROW + 8 * j + 4 * g]);
+              *reinterpret_cast<const f32x4*>(&kl[(32 * st + n32) * KROW + 8 * j + 4 * g]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sacc[st] = mfma_f32(a[e], qf[4 * j + e], sacc[st]);
+          for (int e = 0; e < 4; ++e) sacc[0][st] = mfma_f32(a[e], qf[0][4 * j + e], sacc[0][st]);
         }
-    } else {
+      const int kb = it * BN;
+      if (kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset + q0)) {
+        mask_subtile(sacc, kb, 0);
+        mask_subtile(sacc, kb, 1);
+      }
+      float mx = kNegInf;
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s)
+      for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const u32x4 a =
-              *reinterpret_cast<const u32x4*>(&k_lds[(32 * st + n32) * KROW + 16 * s + 8 * g]);
-          sacc[st] = mfma16<MODE>(a, qf[s], sacc[st]);
-        }
-    }
-
-    // ---- mask keys past this row's end (ragged tail, causal diagonal)
-    const int kb = it * BN;
-    const bool tail = kb + BN > kv_end;
-    const bool diag = p.causal && (kb + BN - 1 > p.q_offset + q0);
-    if (tail || diag) {
-      const int lim = p.causal ? min(kv_end - 1, p.q_offset + qrow) : kv_end - 1;
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[0][st][r], sacc[0][st][r + 1]));
+      const float mx_s = partner_max(mx) * sl2;
+      if (__builtin_amdgcn_ballot_w64(mx_s > m_s[0] + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m_s[0], mx_s);
+        const float corr = fast_exp2(m_s[0] - ((m_new == kNegInf) ? 0.f : m_new));
+        m_s[0] = m_new;
+        l_run[0] *= corr;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) oacc[0][dt] *= corr;
+      }
+      const float mc = (m_s[0] == kNegInf) ? 0.f : m_s[0];
+      float rs = 0.f;
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * st + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key > lim) sacc[st][r] = kNegInf;
+          const float e = fast_exp2(__builtin_fmaf(sacc[0][st][r], sl2, -mc));
+          sacc[0][st][r] = e;
+          rs += e;
         }
-    }
-
-    // ---- online softmax (base 2)
-    float mx = kNegInf;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[st][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;  // row fully masked so far
-    const float corr = fast_exp2((m_run - m_use) * sl2);
-    const float mc = m_use * sl2;
-    float rs = 0.f;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = fast_exp2(__builtin_fmaf(sacc[st][r], sl2, -mc));
-        sacc[st][r] = e;
-        rs += e;
-      }
-    l_run = __builtin_fmaf(l_run, corr, rs);
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= corr;
-
-    // ---- O^T += V^T P^T
-    if constexpr (F32) {
+      l_run[0] += rs;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -470,62 +531,233 @@ __global__ __launch_bounds__(NW * 64) void fwd_kernel(FwdParams p) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const f32x4 a = *reinterpret_cast<const f32x4*>(
-                &v_lds[(32 * dt + n32) * VROW + 32 * st + 8 * j + 4 * g]);
+                &vl[(32 * dt + n32) * VROW + 32 * st + 8 * j + 4 * g]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) oacc[dt] = mfma_f32(a[e], sacc[st][4 * j + e], oacc[dt]);
+            for (int e = 0; e < 4; ++e)
+              oacc[0][dt] = mfma_f32(a[e], sacc[0][st][4 * j + e], oacc[0][dt]);
           }
-    } else {
+      if (it + 1 < t_end) {
+        store_tile(buf ^ 1);
+        if (it + 2 < t_end) load_tile(it + 2);
+      }
+      __syncthreads();
+    }
+  } else {
+    // ---------------------------------------------------------------------------------------
+    // 16-bit: each 64-key tile runs as four MFMA groups, each interleaved with VALU work that
+    // does not depend on it, so the matrix pipe and the exp/FMA pipe run side by side:
+    //   A  S^T(subtile 0)                      then max(0)   [branches live here]
+    //   B  S^T(subtile 1)   || exp/pack/sum(0) then max(1)   [branches live here]
+    //   C  O^T += V^T P^T(0) || exp/pack/sum(1)
+    //   D  O^T += V^T P^T(1) then stage the next tile
+    // Probabilities are packed to 16 bits as they are produced; row sums use v_dot2 on the
+    // packed pairs, i.e. they sum exactly the weights the second product consumes.
+    // ---------------------------------------------------------------------------------------
+    constexpr int NQK = (D / 16) * QW;        // MFMAs per subtile in S^T
+    constexpr int NPV = 2 * (D / 32) * QW;    // MFMAs per subtile in O^T
+    constexpr int EXPO_VALU = QW * 58;        // VALU instructions of one exp/pack/sum step
+    u32x4 pf[QW][4];   // packed P: pf[c][t] = keys 16t..16t+15 of the tile, B-operand order
+    float mc[QW];      // running max to subtract, scaled (0 while a row is fully masked)
+
+    // Transposing-read geometry: in each 16-lane group, lane j reads 4 elements of row
+    // (r0 + j/4) at column (c0 + 4*(j%4)); lane j then holds column c0 + j of rows r0..r0+3.
+    const int jt = lane & 15;
+    const int tr_row = jt >> 2, tr_col = 4 * (jt & 3);
+    const int half16 = 16 * ((lane >> 4) & 1);  // which 16 of the 32 M-rows this group covers
+    auto qk = [&](f32x16 (&sacc)[QW][2], const LT* kl, int st) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const f32x16& sv = sacc[t >> 1];
-        const int o = 8 * (t & 1);
-        const u32x4 pf = {pack2<MODE>(sv[o + 0], sv[o + 1]), pack2<MODE>(sv[o + 2], sv[o + 3]),
-                          pack2<MODE>(sv[o + 4], sv[o + 5]), pack2<MODE>(sv[o + 6], sv[o + 7])};
+      for (int s = 0; s < D / 16; ++s) {
+        u32x4 a;
+        if constexpr (KT) {
+          // K^T tile [d][key]: A(key = 32st + n32, d = 16s + 8g + e)
+          const LT* base = &kl[(16 * s + 8 * g + tr_row) * KTROW + 32 * st + half16 + tr_col];
+          const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
+          a = u32x4{lo.x, lo.y, hi.x, hi.y};
+        } else {
+          a = *reinterpret_cast<const u32x4*>(&kl[(32 * st + n32) * KROW + 16 * s + 8 * g]);
+        }
+#pragma unroll
+        for (int c = 0; c < QW; ++c) sacc[c][st] = mfma16<MODE>(a, qf[c][s], sacc[c][st]);
+      }
+    };
+    // Row max of subtile `st`; raise the running max (rarely) and rescale what depends on it.
+    // When st == 1 the packed weights of subtile 0 are still waiting for their product, so they
+    // are rescaled with the accumulator.
+    auto stat = [&](f32x16 (&sacc)[QW][2], int st) {
+#pragma unroll
+      for (int c = 0; c < QW; ++c) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[c][st][r], sacc[c][st][r + 1]));
+        const float mx_s = partner_max(mx) * sl2;
+        if (__builtin_amdgcn_ballot_w64(mx_s > m_s[c] + kRescaleSlack) != 0) {
+          const float m_new = fmaxf(m_s[c], mx_s);
+          const float corr = fast_exp2(m_s[c] - ((m_new == kNegInf) ? 0.f : m_new));
+          m_s[c] = m_new;
+          l_run[c] *= corr;
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt) oacc[c][dt] *= corr;
+          if (st == 1) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int w = 0; w < 4; ++w) {
+                const uint32_t x = pf[c][t][w];
+                pf[c][t][w] = pack2<MODE>(to_f32<MODE>(x & 0xffffu) * corr,
+                                          to_f32<MODE>(x >> 16) * corr);
+              }
+          }
+        }
+        mc[c] = (m_s[c] == kNegInf) ? 0.f : m_s[c];
+      }
+    };
+    auto expo = [&](f32x16 (&sacc)[QW][2], int st) {
+#pragma unroll
+      for (int c = 0; c < QW; ++c) {
+        float rs = 0.f;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          // Each packed pair is kept in a scalar and the operand tuple is assembled once: reads
+          // of a vector lane through a reference were mis-lowered (every read saw lane 0).
+          uint32_t w[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float e0 = fast_exp2(__builtin_fmaf(sacc[c][st][8 * h2 + 2 * k], sl2, -mc[c]));
+            const float e1 =
+                fast_exp2(__builtin_fmaf(sacc[c][st][8 * h2 + 2 * k + 1], sl2, -mc[c]));
+            const uint32_t pk = pack2<MODE>(e0, e1);
+            w[k] = pk;
+            if constexpr (MODE == kBF16) {
+              rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk),
+                                                   bf16x2{(__bf16)1.f, (__bf16)1.f}, rs, false);
+            } else {
+              rs = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk),
+                                          f16x2{(_Float16)1.f, (_Float16)1.f}, rs, false);
+            }
+          }
+          pf[c][2 * st + h2] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        l_run[c] += rs;
+      }
+    };
+    // Keep the exp/pack/sum work of subtile `st` inside the phase that hides it: without a use
+    // here, LLVM sinks it next to its consumer, past the phase's end.
+    auto pin = [&](int st) {
+#pragma unroll
+      for (int c = 0; c < QW; ++c) {
+        asm volatile("" : "+v"(pf[c][2 * st]), "+v"(pf[c][2 * st + 1]), "+v"(l_run[c]));
+      }
+    };
+    auto pv = [&](const LT* vl, int st) {
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int t = 2 * st + h2;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          const LT* vr = &v_lds[(32 * dt + n32) * VROW + 16 * t + 4 * g];
-          const u32x2 a0 = *reinterpret_cast<const u32x2*>(vr);
-          const u32x2 a1 = *reinterpret_cast<const u32x2*>(vr + 8);
-          oacc[dt] = mfma16<MODE>(u32x4{a0.x, a0.y, a1.x, a1.y}, pf, oacc[dt]);
+          // V tile [key][d]: A(d = 32dt + n32, keys 16t + 4g + e (e < 4), 16t + 8 + 4g + e - 4)
+          const LT* base = &vl[(16 * t + 4 * g + tr_row) * VROW + 32 * dt + half16 + tr_col];
+          const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
+          const u32x4 a = {a0.x, a0.y, a1.x, a1.y};
+#pragma unroll
+          for (int c = 0; c < QW; ++c) oacc[c][dt] = mfma16<MODE>(a, pf[c][t], oacc[c][dt]);
         }
       }
+    };
+
+    for (int it = t_begin; it < t_end; ++it) {
+      const int buf = (it - t_begin) & 1;
+      const LT* kl = k_lds + buf * KBUF;
+      const LT* vl = v_lds + buf * VBUF;
+      const int kb = it * BN;
+      const bool need_mask = kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset + q0);
+      f32x16 sacc[QW][2];
+#pragma unroll
+      for (int c = 0; c < QW; ++c)
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[c][st][r] = 0.f;
+
+      // A
+      qk(sacc, kl, 0);
+      if (need_mask) mask_subtile(sacc, kb, 0);
+      stat(sacc, 0);
+      // B
+      __builtin_amdgcn_sched_barrier(0);
+      qk(sacc, kl, 1);
+      expo(sacc, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, D / 16, 0);  // K fragment reads first
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, EXPO_VALU / NQK, 0);  // then VALU
+      }
+      pin(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (need_mask) mask_subtile(sacc, kb, 1);
+      stat(sacc, 1);
+      // C
+      __builtin_amdgcn_sched_barrier(0);
+      pv(vl, 0);
+      expo(sacc, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, D / 16, 0);  // V fragment reads first
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, EXPO_VALU / NPV, 0);
+      }
+      pin(1);
+      __builtin_amdgcn_sched_barrier(0);
+      // D
+      pv(vl, 1);
+      if (it + 1 < t_end) {
+        store_tile(buf ^ 1);
+        if (it + 2 < t_end) load_tile(it + 2);
+      }
+      __syncthreads();
     }
   }
 
-  // ---- epilogue: oacc[dt][4r + e] <-> d = 32dt + 8r + 4g + e of query qrow
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  if (qrow >= p.Tq) return;
-  if (p.n_split == 1) {
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
-                        (int64_t)qrow * p.o_st;
+  // ---- epilogue: oacc[c][dt][4r + e] <-> d = 32dt + 8r + 4g + e of query q0 + 32c + n32
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+  for (int c = 0; c < QW; ++c) {
+    const float l_tot = partner_sum(l_run[c]);
+    const int qrow = q0 + 32 * c + n32;
+    if (qrow >= p.Tq) continue;
+    if (p.n_split == 1) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
+                          (int64_t)qrow * p.o_st;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const f32x4 x = {oacc[dt][4 * r] * inv, oacc[dt][4 * r + 1] * inv,
-                         oacc[dt][4 * r + 2] * inv, oacc[dt][4 * r + 3] * inv};
-        store4<OUTT>(op + 32 * dt + 8 * r + 4 * g, x, p.o_vec);
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const f32x4 x = {oacc[c][dt][4 * r] * inv, oacc[c][dt][4 * r + 1] * inv,
+                           oacc[c][dt][4 * r + 2] * inv, oacc[c][dt][4 * r + 3] * inv};
+          if (aligned) st4<OUTT, true>(op + 32 * dt + 8 * r + 4 * g, x);
+          else st4<OUTT, false>(op + 32 * dt + 8 * r + 4 * g, x);
+        }
+    } else {
+      const int64_t prow = ((int64_t)(b * p.Hq + h) * p.n_split + split) * p.Tq + qrow;
+      float* wo = p.ws + prow * D;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const f32x4 x = {oacc[c][dt][4 * r], oacc[c][dt][4 * r + 1], oacc[c][dt][4 * r + 2],
+                           oacc[c][dt][4 * r + 3]};
+          *reinterpret_cast<f32x4*>(wo + 32 * dt + 8 * r + 4 * g) = x;
+        }
+      if (g == 0) {
+        float* ml = p.ws + (int64_t)p.B * p.Hq * p.n_split * p.Tq * D + prow * 2;
+        *reinterpret_cast<f32x2*>(ml) = f32x2{m_s[c], l_tot};  // max in scaled log2 units
       }
-  } else {
-    const int64_t prow = ((int64_t)(b * p.Hq + h) * p.n_split + split) * p.Tq + qrow;
-    float* wo = p.ws + prow * D;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const f32x4 x = {oacc[dt][4 * r], oacc[dt][4 * r + 1], oacc[dt][4 * r + 2],
-                         oacc[dt][4 * r + 3]};
-        *reinterpret_cast<f32x4*>(wo + 32 * dt + 8 * r + 4 * g) = x;
-      }
-    if (g == 0) {
-      float* ml = p.ws + (int64_t)p.B * p.Hq * p.n_split * p.Tq * D + prow * 2;
-      *reinterpret_cast<f32x2*>(ml) = f32x2{m_run, l_tot};
     }
   }
 }
 
 // Merge split-key partials by log-sum-exp: one 64-lane workgroup per (batch, head, query row).
+// Partial maxima are in scaled log2 units.
 template <int OUTT, int D>
 __global__ __launch_bounds__(64) void combine_kernel(CombineParams p) {
   const int row = blockIdx.x;
@@ -536,8 +768,12 @@ __global__ __launch_bounds__(64) void combine_kernel(CombineParams p) {
   const float* wo = p.ws + base * D;
   const float* ml = p.ws + (int64_t)p.B * p.Hq * p.n_split * p.Tq * D + base * 2;
   const int64_t so = (int64_t)p.Tq * D, sml = (int64_t)p.Tq * 2;
+  // every lane loads one split's (m, l) so the loads are issued together
+  const int lane = threadIdx.x;
   float m = kNegInf;
-  for (int s = 0; s < p.n_split; ++s) m = fmaxf(m, ml[s * sml]);
+  for (int s = lane; s < p.n_split; s += 64) m = fmaxf(m, ml[s * sml]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   const float mu = (m == kNegInf) ? 0.f : m;
   constexpr int PER = D / 64;
   float acc[PER];
@@ -545,10 +781,10 @@ __global__ __launch_bounds__(64) void combine_kernel(CombineParams p) {
   for (int i = 0; i < PER; ++i) acc[i] = 0.f;
   float l = 0.f;
   for (int s = 0; s < p.n_split; ++s) {
-    const float w = fast_exp2((ml[s * sml] - mu) * p.scale_log2);
+    const float w = fast_exp2(ml[s * sml] - mu);
     l = __builtin_fmaf(w, ml[s * sml + 1], l);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) acc[i] = __builtin_fmaf(w, wo[s * so + threadIdx.x + 64 * i], acc[i]);
+    for (int i = 0; i < PER; ++i) acc[i] = __builtin_fmaf(w, wo[s * so + lane + 64 * i], acc[i]);
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   store_t<OUTT>* op =
@@ -556,8 +792,8 @@ __global__ __launch_bounds__(64) void combine_kernel(CombineParams p) {
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const float x = acc[i] * inv;
-    if constexpr (OUTT == kF32) op[threadIdx.x + 64 * i] = x;
-    else op[threadIdx.x + 64 * i] = (uint16_t)from_f32<OUTT>(x);
+    if constexpr (OUTT == kF32) op[lane + 64 * i] = x;
+    else op[lane + 64 * i] = from_f32<OUTT>(x);
   }
 }
 

@@ -27,7 +27,7 @@ struct FwdParams {
   int32_t n_split;           // key splits per (b, h, q-block); 1 = no partials
   int32_t tiles_per_split;   // key tiles (of 64) per split
   int32_t n_work;            // B * Hq * n_qblk * n_split logical workgroups
-  int32_t q_vec, k_vec, v_vec, o_vec;  // widest aligned access, in elements (1, 2, 4, 8)
+  int32_t aligned;           // every operand admits the kernels' vector loads and stores
   float scale_log2;          // scale * log2(e)
 };
 
@@ -36,27 +36,32 @@ struct CombineParams {
   void* o;
   int64_t o_sb, o_sh, o_st;
   int32_t B, Hq, Tq, n_split;
-  float scale_log2;
 };
 
 // Launchers; return hipSuccess or the launch error.
 // mode: kBF16 / kF16 (MFMA bf16/f16 kernel, q and kv the same 16-bit type) or kF32 (f32 MFMA
 // kernel; kv may be f32, f16 or bf16, widened to f32 as it is staged).
 // out_dtype: kF32, kF16 or kBF16. k_transposed: K^T layout.
+// variant: launch shape (see Variant).
+enum Variant : int {
+  kWave1 = 0,   // 1 wave x 32 query rows per workgroup (decode, short queries)
+  kWave4 = 1,   // 4 waves x 32 rows (128 rows; head_dim 128 and the f32 kernel)
+  kWave4x2 = 2  // 4 waves x 64 rows (256 rows; 16-bit head_dim 64: two column blocks per wave)
+};
+inline int block_m_of(int variant) { return variant == kWave1 ? 32 : variant == kWave4 ? 128 : 256; }
+
 hipError_t launch_fwd(const FwdParams& p, int mode, int kv_dtype, int out_dtype, int head_dim,
-                      bool k_transposed, int waves, hipStream_t stream);
+                      bool k_transposed, int variant, hipStream_t stream);
 hipError_t launch_combine(const CombineParams& p, int out_dtype, int head_dim,
                           hipStream_t stream);
 // Per-dtype instantiation units (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip).
-hipError_t launch_fwd_bf16(const FwdParams& p, int out_dtype, int d, bool kt, int waves,
+hipError_t launch_fwd_bf16(const FwdParams& p, int out_dtype, int d, bool kt, int variant,
                            hipStream_t s);
-hipError_t launch_fwd_f16(const FwdParams& p, int out_dtype, int d, bool kt, int waves,
+hipError_t launch_fwd_f16(const FwdParams& p, int out_dtype, int d, bool kt, int variant,
                           hipStream_t s);
-hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int waves,
+hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int variant,
                           hipStream_t s);
 
-// Query rows per workgroup for a kernel shape: 32 per wave.
-inline int block_m_for(int waves) { return 32 * waves; }
 constexpr int kBlockN = 64;  // keys per tile
 
 }  // namespace ffai

@@ -3,10 +3,10 @@
 
 namespace ffai {
 
-hipError_t launch_fwd_bf16(const FwdParams& p, int out_dtype, int d, bool kt, int waves,
+hipError_t launch_fwd_bf16(const FwdParams& p, int out_dtype, int d, bool kt, int variant,
                             hipStream_t s) {
-  if (out_dtype == kBF16) return pick_dim<kBF16, kBF16, kBF16>(p, d, kt, waves, s);
-  if (out_dtype == kF32) return pick_dim<kBF16, kBF16, kF32>(p, d, kt, waves, s);
+  if (out_dtype == kBF16) return pick_dim<kBF16, kBF16, kBF16>(p, d, kt, variant, s);
+  if (out_dtype == kF32) return pick_dim<kBF16, kBF16, kF32>(p, d, kt, variant, s);
   return hipErrorInvalidValue;
 }
 

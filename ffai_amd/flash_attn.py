@@ -97,10 +97,16 @@ def attend_merged(q: torch.Tensor, kt: torch.Tensor,
                   v: torch.Tensor) -> Optional[torch.Tensor]:
     """flash_attn::attend_merged: encoder attention writing (1,T,H*64) f32 directly, or None."""
     lib = L.load()
+    qv, kv, vv = _view(q), _view(kt), _view(v)
     heads, seq = q.shape[1], q.shape[2]
     out = torch.empty(1, seq, heads * 64, dtype=torch.float32, device=q.device)
-    rc = lib.ffai_attend_merged(ctypes.byref(_view(q)), ctypes.byref(_view(kt)),
-                                ctypes.byref(_view(v)), ctypes.byref(_view(out)),
+    nbytes = ctypes.c_size_t(0)
+    rc = lib.ffai_attend_merged_workspace_bytes(ctypes.byref(qv), ctypes.byref(kv),
+                                                ctypes.byref(vv), ctypes.byref(nbytes))
+    ws = _workspace(nbytes.value, q.device) if rc == L.FFAI_OK else None
+    rc = lib.ffai_attend_merged(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv),
+                                ctypes.byref(_view(out)),
+                                None if ws is None else ws.data_ptr(), nbytes.value,
                                 _stream_handle(q))
     if L.check(rc) == L.FFAI_DECLINED:
         return None

@@ -130,9 +130,14 @@ int ffai_attend_workspace_bytes(const ffai_tensor* q, const ffai_tensor* kt,
 
 /* flash_attn::attend_merged (flash_attn.rs:131-158 + MergedAttnOp, :160-210): encoder
  * attention writing the merged (1,T,H*64) f32 layout. Declines unless batch 1, head_dim 64,
- * all f32, qlen == keys >= 256. */
+ * all f32, qlen == keys >= 256. The workspace (see ffai_attend_merged_workspace_bytes) holds
+ * split-key partials when few heads leave the GPU short of work. */
 int ffai_attend_merged(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor* v,
-                       ffai_tensor* out, void* stream);
+                       ffai_tensor* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace ffai_attend_merged needs for these operands (0 if none or if it would decline). */
+int ffai_attend_merged_workspace_bytes(const ffai_tensor* q, const ffai_tensor* kt,
+                                       const ffai_tensor* v, size_t* bytes);
 
 /* Knob mirror of knobs::DECODE_MIN_KEYS (knobs.rs:163-168): key-count floor below which the
  * decode shape declines. Initialised from FFAI_DECODE_MIN_KEYS (default 8) on first use. */

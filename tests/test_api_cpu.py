@@ -168,7 +168,7 @@ def test_attend_merged_decline_rules(lib):
 
     def rc(q, kt, v):
         return lib.ffai_attend_merged(ctypes.byref(q), ctypes.byref(kt), ctypes.byref(v),
-                                      ctypes.byref(out), None)
+                                      ctypes.byref(out), None, 0, None)
 
     ok = (view((1, 4, 300, 64)), view((1, 4, 64, 300)), view((1, 4, 300, 64)))
     assert rc(view((1, 4, 300, 64), dtype=L.BF16), ok[1], ok[2]) == L.FFAI_DECLINED
