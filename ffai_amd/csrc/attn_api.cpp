@@ -151,6 +151,14 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split) {
   if (!f32 && d->head_dim == 64 && d->q_len >= 256) p.variant = ffai::kWave4x2;
   if (p.variant == ffai::kWave4x2 && work_of(p.variant) < 256) p.variant = ffai::kWave4;
   if (p.variant == ffai::kWave4 && work_of(p.variant) < 256) p.variant = ffai::kWave1;
+  // FFAI_ATTN_VARIANT (0, 1, 2) forces a launch shape where it is instantiated: a tuning knob.
+  static const int forced = [] {
+    const char* e = std::getenv("FFAI_ATTN_VARIANT");
+    return (e && e[0] >= '0' && e[0] <= '2' && e[1] == '\0') ? e[0] - '0' : -1;
+  }();
+  if (forced == ffai::kWave1 || forced == ffai::kWave4 ||
+      (forced == ffai::kWave4x2 && !f32 && d->head_dim == 64))
+    p.variant = forced;
   const int64_t work = work_of(p.variant);
   const int bm = ffai::block_m_of(p.variant);
   p.n_qblk = (d->q_len + bm - 1) / bm;

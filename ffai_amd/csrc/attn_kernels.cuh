@@ -209,12 +209,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   // LDS tiles, rows padded so that the 128-bit stores and the MFMA operand reads are
   // bank-conflict free.
   //   f32:    K [key][d] (KROW = D + 4), V^T [d][key] (VROW = BN + 4) - transposed on the way in.
-  //   16-bit: K [key][d] (KROW = D + 8) when K comes as rows, K^T [d][key] (KTROW = BN + 16) when
-  //           it comes transposed, V [key][d] (VROW = D + 16): all stored as they come, and the
+  //   16-bit: K [key][d] (KROW = D + 8) when K comes as rows, K^T [d][key] (KTROW = BN + 32) when
+  //           it comes transposed, V [key][d] (VROW = D + 32): all stored as they come, and the
   //           operands that need the other orientation are read with ds_read_b64_tr_b16.
   constexpr int KROW = F32 ? D + 4 : D + 8;
-  constexpr int KTROW = BN + 16;
-  constexpr int VROW = F32 ? BN + 4 : D + 16;
+  constexpr int KTROW = BN + 32;
+  constexpr int VROW = F32 ? BN + 4 : D + 32;
   constexpr int KBUF = (!F32 && KT) ? D * KTROW : BN * KROW;
   constexpr int VBUF = F32 ? D * VROW : BN * VROW;
   __shared__ __attribute__((aligned(16))) LT k_lds[2 * KBUF];
@@ -546,98 +546,96 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // ---------------------------------------------------------------------------------------
     // 16-bit: each 64-key tile runs as four MFMA groups, each interleaved with VALU work that
     // does not depend on it, so the matrix pipe and the exp/FMA pipe run side by side:
-    //   A  S^T(subtile 0)                      then max(0)   [branches live here]
-    //   B  S^T(subtile 1)   || exp/pack/sum(0) then max(1)   [branches live here]
-    //   C  O^T += V^T P^T(0) || exp/pack/sum(1)
+    //   A  S^T(subtile 0)
+    //   B  S^T(subtile 1)    || max/exp/pack/sum(0)   then rescale O (rare branch)
+    //   C  O^T += V^T P^T(0) || max/exp/pack/sum(1)   then rescale O (rare branch)
     //   D  O^T += V^T P^T(1) then stage the next tile
     // Probabilities are packed to 16 bits as they are produced; row sums use v_dot2 on the
     // packed pairs, i.e. they sum exactly the weights the second product consumes.
     // ---------------------------------------------------------------------------------------
     constexpr int NQK = (D / 16) * QW;        // MFMAs per subtile in S^T
     constexpr int NPV = 2 * (D / 32) * QW;    // MFMAs per subtile in O^T
-    constexpr int EXPO_VALU = QW * 58;        // VALU instructions of one exp/pack/sum step
+    constexpr int EXPO_VALU = QW * 72;        // VALU instructions of one max/exp/pack/sum step
     u32x4 pf[QW][4];   // packed P: pf[c][t] = keys 16t..16t+15 of the tile, B-operand order
-    float mc[QW];      // running max to subtract, scaled (0 while a row is fully masked)
 
     // Transposing-read geometry: in each 16-lane group, lane j reads 4 elements of row
     // (r0 + j/4) at column (c0 + 4*(j%4)); lane j then holds column c0 + j of rows r0..r0+3.
     const int jt = lane & 15;
     const int tr_row = jt >> 2, tr_col = 4 * (jt & 3);
     const int half16 = 16 * ((lane >> 4) & 1);  // which 16 of the 32 M-rows this group covers
+    // A operand of S^T for subtile st, contraction step s: K(key = 32st + n32, d = 16s + 8g + e).
+    auto kfrag = [&](const LT* kl, int st, int s) -> u32x4 {
+      if constexpr (KT) {
+        const LT* base = &kl[(16 * s + 8 * g + tr_row) * KTROW + 32 * st + half16 + tr_col];
+        const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
+        return u32x4{lo.x, lo.y, hi.x, hi.y};
+      } else {
+        return *reinterpret_cast<const u32x4*>(&kl[(32 * st + n32) * KROW + 16 * s + 8 * g]);
+      }
+    };
     auto qk = [&](f32x16 (&sacc)[QW][2], const LT* kl, int st) {
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) {
-        u32x4 a;
-        if constexpr (KT) {
-          // K^T tile [d][key]: A(key = 32st + n32, d = 16s + 8g + e)
-          const LT* base = &kl[(16 * s + 8 * g + tr_row) * KTROW + 32 * st + half16 + tr_col];
-          const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
-          a = u32x4{lo.x, lo.y, hi.x, hi.y};
-        } else {
-          a = *reinterpret_cast<const u32x4*>(&kl[(32 * st + n32) * KROW + 16 * s + 8 * g]);
-        }
+        const u32x4 a = kfrag(kl, st, s);
 #pragma unroll
         for (int c = 0; c < QW; ++c) sacc[c][st] = mfma16<MODE>(a, qf[c][s], sacc[c][st]);
       }
     };
-    // Row max of subtile `st`; raise the running max (rarely) and rescale what depends on it.
-    // When st == 1 the packed weights of subtile 0 are still waiting for their product, so they
-    // are rescaled with the accumulator.
-    auto stat = [&](f32x16 (&sacc)[QW][2], int st) {
+    float corr_s[QW];  // accumulator rescale owed by the last max update of column block c
+    // Weights of column block c, subtile st, from its 16 scores `sv`. The running max is raised
+    // without a branch, and lazily: only when a score exceeds it by more than kRescaleSlack
+    // (log2 units), so the weights stay below 2^kRescaleSlack and the rescale the accumulator
+    // then owes (corr_s) is rare. The row sum takes the rescale at once; the accumulator takes
+    // it in `rescale`, after the products that used the previous weights were issued.
+    auto expo_c = [&](const f32x16& sv, int c, int st) {
+      float mx = kNegInf;
 #pragma unroll
-      for (int c = 0; c < QW; ++c) {
-        float mx = kNegInf;
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sv[r], sv[r + 1]));
+      const float mx_s = partner_max(mx) * sl2;
+      const float m_old = m_s[c];
+      const float m_new = (mx_s > m_old + kRescaleSlack) ? mx_s : m_old;
+      const float corr = (m_new == m_old) ? 1.f : fast_exp2(m_old - m_new);
+      m_s[c] = m_new;
+      corr_s[c] = corr;
+      const float mc = (m_new == kNegInf) ? 0.f : m_new;
+      float rs = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[c][st][r], sacc[c][st][r + 1]));
-        const float mx_s = partner_max(mx) * sl2;
-        if (__builtin_amdgcn_ballot_w64(mx_s > m_s[c] + kRescaleSlack) != 0) {
-          const float m_new = fmaxf(m_s[c], mx_s);
-          const float corr = fast_exp2(m_s[c] - ((m_new == kNegInf) ? 0.f : m_new));
-          m_s[c] = m_new;
-          l_run[c] *= corr;
+      for (int h2 = 0; h2 < 2; ++h2) {
+        // Each packed pair is kept in a scalar and the operand tuple is assembled once: reads of
+        // a vector lane through a reference were mis-lowered (every read saw lane 0).
+        uint32_t w[4];
 #pragma unroll
-          for (int dt = 0; dt < D / 32; ++dt) oacc[c][dt] *= corr;
-          if (st == 1) {
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-              for (int w = 0; w < 4; ++w) {
-                const uint32_t x = pf[c][t][w];
-                pf[c][t][w] = pack2<MODE>(to_f32<MODE>(x & 0xffffu) * corr,
-                                          to_f32<MODE>(x >> 16) * corr);
-              }
+        for (int k = 0; k < 4; ++k) {
+          const float e0 = fast_exp2(__builtin_fmaf(sv[8 * h2 + 2 * k], sl2, -mc));
+          const float e1 = fast_exp2(__builtin_fmaf(sv[8 * h2 + 2 * k + 1], sl2, -mc));
+          const uint32_t pk = pack2<MODE>(e0, e1);
+          w[k] = pk;
+          if constexpr (MODE == kBF16) {
+            rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk),
+                                                 bf16x2{(__bf16)1.f, (__bf16)1.f}, rs, false);
+          } else {
+            rs = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk),
+                                        f16x2{(_Float16)1.f, (_Float16)1.f}, rs, false);
           }
         }
-        mc[c] = (m_s[c] == kNegInf) ? 0.f : m_s[c];
+        pf[c][2 * st + h2] = u32x4{w[0], w[1], w[2], w[3]};
       }
+      l_run[c] = __builtin_fmaf(l_run[c], corr, rs);
     };
     auto expo = [&](f32x16 (&sacc)[QW][2], int st) {
 #pragma unroll
-      for (int c = 0; c < QW; ++c) {
-        float rs = 0.f;
+      for (int c = 0; c < QW; ++c) expo_c(sacc[c][st], c, st);
+    };
+    // Apply the owed rescale to the accumulator (whole wave, only when some row owes one).
+    auto rescale = [&]() {
+      bool any = false;
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          // Each packed pair is kept in a scalar and the operand tuple is assembled once: reads
-          // of a vector lane through a reference were mis-lowered (every read saw lane 0).
-          uint32_t w[4];
+      for (int c = 0; c < QW; ++c) any = any || corr_s[c] != 1.f;
+      if (__builtin_amdgcn_ballot_w64(any) != 0) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float e0 = fast_exp2(__builtin_fmaf(sacc[c][st][8 * h2 + 2 * k], sl2, -mc[c]));
-            const float e1 =
-                fast_exp2(__builtin_fmaf(sacc[c][st][8 * h2 + 2 * k + 1], sl2, -mc[c]));
-            const uint32_t pk = pack2<MODE>(e0, e1);
-            w[k] = pk;
-            if constexpr (MODE == kBF16) {
-              rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk),
-                                                   bf16x2{(__bf16)1.f, (__bf16)1.f}, rs, false);
-            } else {
-              rs = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk),
-                                          f16x2{(_Float16)1.f, (_Float16)1.f}, rs, false);
-            }
-          }
-          pf[c][2 * st + h2] = u32x4{w[0], w[1], w[2], w[3]};
-        }
-        l_run[c] += rs;
+        for (int c = 0; c < QW; ++c)
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt) oacc[c][dt] *= corr_s[c];
       }
     };
     // Keep the exp/pack/sum work of subtile `st` inside the phase that hides it: without a use
@@ -645,7 +643,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     auto pin = [&](int st) {
 #pragma unroll
       for (int c = 0; c < QW; ++c) {
-        asm volatile("" : "+v"(pf[c][2 * st]), "+v"(pf[c][2 * st + 1]), "+v"(l_run[c]));
+        asm volatile("" : "+v"(pf[c][2 * st]), "+v"(pf[c][2 * st + 1]), "+v"(l_run[c]),
+                     "+v"(corr_s[c]));
       }
     };
     auto pv = [&](const LT* vl, int st) {
@@ -681,7 +680,6 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       // A
       qk(sacc, kl, 0);
       if (need_mask) mask_subtile(sacc, kb, 0);
-      stat(sacc, 0);
       // B
       __builtin_amdgcn_sched_barrier(0);
       qk(sacc, kl, 1);
@@ -694,8 +692,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       }
       pin(0);
       __builtin_amdgcn_sched_barrier(0);
+      rescale();
       if (need_mask) mask_subtile(sacc, kb, 1);
-      stat(sacc, 1);
       // C
       __builtin_amdgcn_sched_barrier(0);
       pv(vl, 0);
@@ -708,6 +706,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       }
       pin(1);
       __builtin_amdgcn_sched_barrier(0);
+      rescale();
       // D
       pv(vl, 1);
       if (it + 1 < t_end) {
