@@ -8,10 +8,13 @@ calls. FLOP = 4 * B * H * T^2 * D per layer (flash_probe.rs:432's convention).
 
 Also reported: the beam-5 decode step at the whisper-medium shape (24 layers of decoder
 self-attention over ragged per-beam caches plus cross-attention over 1500 shared encoder frames,
-bf16 K/V, f32 output), the whisper-tiny f32 encoder, and the CPU oracle (the reference's
-algorithm restated in C++/AVX2) timed on this host's cores on a bounded sample.
+bf16 K/V, f32 output), the whisper-tiny f32 and whisper-small bf16 encoders, the
+Qwen2-VL-2B-shape causal prefill (12 query heads over 2 K/V heads, head_dim 128, S = 4096), and
+the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this host's cores on a
+bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras]
+                       [--layers L] [--legs decode,tiny,small,prefill | none | copy]
 """
 
 from __future__ import annotations
@@ -38,6 +41,10 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--legs", default="decode,tiny,small,prefill",
+                    help="comma list of extra legs beside the headline encoder run: decode, "
+                         "tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
+                         "calibration used to scale HBM byte counters")
     return ap.parse_args()
 
 
@@ -50,26 +57,35 @@ def log(*a):
 # ------------------------------------------------------------------------------------------
 
 def encoder_bench(torch, fa, steps, warmup, layers, B=16, H=20, T=1500, D=64,
-                  dtype="bf16"):
+                  dtype="bf16", seed=4, causal=False, H_kv=None, k_mult=1.0):
+    """Self-attention over `layers` distinct buffer sets. K is given transposed (B,Hkv,D,T) as
+    the reference's encoder produces it, except for the causal prefill (rows, as a decoder's
+    cache holds it). FLOP counts only the visible query-key pairs."""
     dev = torch.device("cuda:0")
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
-    g = torch.Generator(device=dev).manual_seed(4)
+    H_kv = H_kv or H
+    kt_layout = not causal
+    g = torch.Generator(device=dev).manual_seed(seed)
     bufs = []
     for _ in range(layers):
         q = torch.randn(B, H, T, D, generator=g, device=dev).to(tdt)
-        kt = torch.randn(B, H, D, T, generator=g, device=dev).to(tdt)
-        v = torch.randn(B, H, T, D, generator=g, device=dev).to(tdt)
+        if kt_layout:
+            k = (torch.randn(B, H_kv, D, T, generator=g, device=dev) * k_mult).to(tdt)
+        else:
+            k = (torch.randn(B, H_kv, T, D, generator=g, device=dev) * k_mult).to(tdt)
+        v = torch.randn(B, H_kv, T, D, generator=g, device=dev).to(tdt)
         o = torch.empty(B, H, T, D, device=dev, dtype=tdt)
-        bufs.append((q, kt, v, o))
+        bufs.append((q, k, v, o))
     scale = D ** -0.5
     ws = None
-    nbytes = fa.workspace_bytes(*bufs[0], k_transposed=True, scale=scale)
+    nbytes = fa.workspace_bytes(*bufs[0], k_transposed=kt_layout, scale=scale, causal=causal)
     if nbytes:
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
 
     def step():
-        for q, kt, v, o in bufs:
-            r = fa.attention(q, kt, v, k_transposed=True, scale=scale, out=o, workspace=ws)
+        for q, k, v, o in bufs:
+            r = fa.attention(q, k, v, k_transposed=kt_layout, scale=scale, causal=causal, out=o,
+                             workspace=ws)
             assert r is not None
 
     for _ in range(warmup):
@@ -86,9 +102,11 @@ def encoder_bench(torch, fa, steps, warmup, layers, B=16, H=20, T=1500, D=64,
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = e0.elapsed_time(e1)
-    flop_layer = 4.0 * B * H * T * T * D
+    pairs = T * (T + 1) / 2 if causal else T * T
+    flop_layer = 4.0 * B * H * pairs * D
     launches = steps * layers
     avg_launch_s = gpu_ms * 1e-3 / launches
+    esz = 2 if dtype == "bf16" else 4
     return {
         "elapsed_s": wall,
         "gpu_ms": gpu_ms,
@@ -96,8 +114,32 @@ def encoder_bench(torch, fa, steps, warmup, layers, B=16, H=20, T=1500, D=64,
         "tflops": flop_layer * launches / (gpu_ms * 1e-3) / 1e12,
         "flop_per_launch": flop_layer,
         "avg_launch_us": avg_launch_s * 1e6,
-        "bytes_per_launch": 4.0 * B * H * T * D * (2 if dtype == "bf16" else 4),
+        "bytes_per_launch": float(B * T * D * esz * (2 * H + 2 * H_kv)),
     }
+
+
+# ------------------------------------------------------------------------------------------
+# Copy calibration: a plain device copy of known size, for scaling the HBM byte counters
+# ------------------------------------------------------------------------------------------
+
+def copy_bench(torch, steps, nbytes=1 << 30):
+    """Copies `nbytes` between two device buffers `steps` times (torch's copy kernel). Under
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE each dispatch should read and write `nbytes`; the
+    ratio of counted to known bytes is the scale applied to the attention kernels' counters."""
+    dev = torch.device("cuda:0")
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"bytes_each_way": nbytes, "us_per_copy": ms * 1e3,
+            "gbps": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
 # ------------------------------------------------------------------------------------------
@@ -255,25 +297,40 @@ def main():
     from ffai_amd import _lib
 
     _lib.load()
+    legs = set() if args.skip_extras else {x for x in args.legs.split(",") if x and x != "none"}
+    if legs == {"copy"}:
+        print(json.dumps({"copy_calibration": copy_bench(torch, max(args.steps, 1))}), flush=True)
+        return
     log("encoder: whisper-large-v3 bf16 ...")
     enc = encoder_bench(torch, fa, args.steps, args.warmup, args.layers)
     log(f"encoder: {enc['tflops']:.1f} TFLOP/s, {enc['ms_per_step']:.3f} ms/step")
     extras = {}
-    if not args.skip_extras:
+    if "decode" in legs:
         log("decode: beam-5 whisper-medium step ...")
         dec = decode_bench(torch, fa, max(args.steps * 10, 100), 10)
         log(f"decode: {dec['us_per_step']:.1f} us/step, {dec['gbps']:.0f} GB/s")
         extras["decode_beam5"] = dec
+    if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")
         tiny = encoder_bench(torch, fa, max(args.steps * 5, 50), args.warmup, 4, B=1, H=6,
-                             dtype="f32")
+                             dtype="f32", seed=1)
         tiny["frac_of_f32_peak"] = tiny["tflops"] / PEAK_F32_TFLOPS
         extras["encoder_tiny_f32"] = tiny
         log(f"tiny f32: {tiny['tflops']:.2f} TFLOP/s")
+    if "small" in legs:
         log("encoder: whisper-small bf16 ...")
-        small = encoder_bench(torch, fa, args.steps, args.warmup, 4, B=8, H=12)
+        small = encoder_bench(torch, fa, args.steps, args.warmup, 4, B=8, H=12, seed=2,
+                              k_mult=2.0)
+        small["frac_of_bf16_peak"] = small["tflops"] / PEAK_BF16_TFLOPS
         extras["encoder_small_bf16"] = small
         log(f"small bf16: {small['tflops']:.1f} TFLOP/s")
+    if "prefill" in legs:
+        log("prefill: qwen2-vl causal GQA bf16 ...")
+        pre = encoder_bench(torch, fa, args.steps, args.warmup, 4, B=1, H=12, H_kv=2, T=4096,
+                            D=128, seed=5, causal=True)
+        pre["frac_of_bf16_peak"] = pre["tflops"] / PEAK_BF16_TFLOPS
+        extras["prefill_causal_gqa_d128"] = pre
+        log(f"prefill: {pre['tflops']:.1f} TFLOP/s")
     cpu = None
     if not args.skip_cpu:
         log("cpu baseline ...")
