@@ -1,7 +1,8 @@
 """Build the gfx950 attention library in-tree: ffai_amd/libffai_attn.so.
 
-One hipcc invocation compiles the kernels (attn_kernels.hip) and the C ABI (attn_api.cpp) for
-gfx950 only. Packed-FP32 VALU instructions are disabled for all device code.
+hipcc compiles the kernel instantiations (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip), the launch
+dispatch (attn_launch.hip) and the C ABI (attn_api.cpp) for gfx950 only, in parallel, then links
+them into one shared library. Packed-FP32 VALU instructions are disabled for all device code.
 """
 
 from __future__ import annotations
