@@ -18,7 +18,8 @@ ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libffai_attn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = [os.path.join(CSRC, n) for n in
-           ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "attn_launch.hip", "attn_api.cpp")]
+           ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "attn_launch.hip",
+            "attn_api.cpp")]
 ARCH = "gfx950"
 
 

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdlib>
@@ -124,6 +125,8 @@ int vec_of(const void* base, size_t esize, const int64_t* strides, int max_vec) 
 }
 
 struct Plan {
+  bool decode;  // decode_kernel (few rows per kv-head) instead of fwd_kernel
+  int waves;    // decode: waves per workgroup
   int variant;
   int n_qblk;
   int n_split;
@@ -132,13 +135,51 @@ struct Plan {
   size_t ws_bytes;
 };
 
-// Launch shape. Long 16-bit head_dim-64 queries: 4 waves x 64 rows per workgroup; other long
-// queries: 4 waves x 32 rows; short ones (decode): 1 wave x 32 rows. A shape that leaves the
-// 256 CUs short of workgroups steps down, then splits the keys: to >= 512 workgroups for the
-// 16-bit kernels, to >= 4096 waves for the f32 kernel, whose long MFMA chains need several
-// waves per SIMD to stay busy.
-Plan make_plan(const ffai_attn_desc* d, bool allow_split) {
+// Decode launch: 16-bit inputs and at most 32 query rows per (batch, kv-head), so one MFMA
+// column block holds every row that reads a K/V head. A workgroup of 8 waves (4 at head_dim
+// 128, for LDS) gives one 64-key tile to each wave; a unit with more tiles than that is split
+// over workgroups whose partials decode_combine_kernel merges. When the units alone leave the
+// GPU short of workgroups, a workgroup takes fewer tiles so that more of them stream keys.
+bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
+  const int group = d->heads_q / d->heads_kv;
+  const int64_t rows = (int64_t)group * d->q_len;
+  if (d->q_dtype == FFAI_F32 || rows > 32 || !allow_split) return false;
+  if (d->k_layout == FFAI_K_TRANSPOSED && d->kv_len < 4) return false;  // 4-key chunk loads
+  const int64_t units = (int64_t)d->batch * d->heads_kv;
+  int64_t kv_blk = d->kv_len;
+  if (d->causal) kv_blk = std::min<int64_t>(kv_blk, (int64_t)d->q_offset + d->q_len);
+  const int64_t n_tiles = std::max<int64_t>(1, (kv_blk + ffai::kBlockN - 1) / ffai::kBlockN);
+  const int waves = d->head_dim == 64 ? 8 : 4;
+  constexpr int64_t kTargetWorkgroups = 64;
+  int64_t tps = waves;
+  if (units * ((n_tiles + tps - 1) / tps) < kTargetWorkgroups)
+    tps = std::max<int64_t>(1, n_tiles * units / kTargetWorkgroups);
+  // FFAI_DECODE_TILES_PER_WG (> 0) forces the 64-key tiles per decode workgroup: a tuning knob.
+  static const int forced_tps = [] {
+    const char* e = std::getenv("FFAI_DECODE_TILES_PER_WG");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced_tps > 0) tps = forced_tps;
+  tps = std::min(tps, n_tiles);
+  // the combine stages all of a unit's partials in LDS
+  const int64_t max_splits = std::max<int64_t>(1, ffai::kCombineLdsFloats / (rows * (d->head_dim + 2)));
+  if ((n_tiles + tps - 1) / tps > max_splits) tps = (n_tiles + max_splits - 1) / max_splits;
+  p->decode = true;
+  p->waves = waves;
+  p->variant = 0;
+  p->n_qblk = 1;
+  p->tiles_per_split = (int)tps;
+  p->n_split = (int)((n_tiles + tps - 1) / tps);
+  p->n_work = (int)(units * p->n_split);
+  p->ws_bytes = p->n_split > 1 ? (size_t)units * p->n_split * rows * (d->head_dim + 2) * 4 : 0;
+  return true;
+}
+
+// `vector_ok`: the operands admit the decode kernel's vector accesses (it has no element-wise
+// path; misaligned decode shapes take fwd_kernel).
+Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok) {
   Plan p{};
+  if (vector_ok && plan_decode(d, allow_split, &p)) return p;
   const int64_t bh = (int64_t)d->batch * d->heads_q;
   const bool f32 = d->q_dtype == FFAI_F32;
   const int n_tiles = (d->kv_len + ffai::kBlockN - 1) / ffai::kBlockN;
@@ -178,6 +219,11 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split) {
   return p;
 }
 
+// Workspace for a descriptor whatever the operands' alignment turns out to be.
+size_t plan_ws_bytes(const ffai_attn_desc* d) {
+  return std::max(make_plan(d, true, true).ws_bytes, make_plan(d, true, false).ws_bytes);
+}
+
 int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v, void* out,
             void* ws, size_t ws_bytes, void* stream, bool allow_split) {
   g_last_error.clear();
@@ -192,11 +238,44 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   const int dev = check_device();
   if (dev != FFAI_OK) return dev;
 
-  const Plan pl = make_plan(d, allow_split);
+  const bool f32 = d->q_dtype == FFAI_F32;
+  const bool kt = d->k_layout == FFAI_K_TRANSPOSED;
+  // The kernels' vector accesses: Q rows 16 B (4 f32 or 8 16-bit elements); K rows and V rows
+  // 16 B in the 16-bit kernels, 4 elements in the f32 kernel; K^T rows 4 keys; O 4 elements.
+  const int need_q = f32 ? 4 : 8, need_kv = f32 ? 4 : 8, need_k = kt ? 4 : need_kv;
+  const bool aligned = vec_of(q, qs, d->q_strides, need_q) == need_q &&
+                       vec_of(k, ks, d->k_strides, need_k) == need_k &&
+                       vec_of(v, ks, d->v_strides, need_kv) == need_kv &&
+                       vec_of(out, os, d->o_strides, 4) == 4;
+
+  const Plan pl = make_plan(d, allow_split, aligned);
   if (pl.ws_bytes > 0) {
     if (!ws || ws_bytes < pl.ws_bytes)
       return fail(FFAI_ERR_WORKSPACE, "workspace smaller than ffai_attn_workspace_bytes");
     if ((uintptr_t)ws % 16) return fail(FFAI_ERR_INVALID, "workspace must be 16-byte aligned");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int mode = f32 ? ffai::kF32 : (d->q_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
+  const int kvt = d->kv_dtype == FFAI_F32 ? ffai::kF32 : (d->kv_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
+  const int ot = d->out_dtype == FFAI_F32 ? ffai::kF32 : (d->out_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
+
+  if (pl.decode) {
+    ffai::DecodeParams p{};
+    p.q = q; p.k = k; p.v = v; p.o = out;
+    p.ws = static_cast<float*>(ws);
+    p.kv_lens = d->kv_lens;
+    p.q_sb = d->q_strides[0]; p.q_sh = d->q_strides[1]; p.q_st = d->q_strides[2];
+    p.k_sb = d->k_strides[0]; p.k_sh = d->k_strides[1]; p.k_st = d->k_strides[2];
+    p.v_sb = d->v_strides[0]; p.v_sh = d->v_strides[1]; p.v_st = d->v_strides[2];
+    p.o_sb = d->o_strides[0]; p.o_sh = d->o_strides[1]; p.o_st = d->o_strides[2];
+    p.B = d->batch; p.Hkv = d->heads_kv; p.group = d->heads_q / d->heads_kv;
+    p.Tq = d->q_len; p.Tk = d->kv_len;
+    p.causal = d->causal; p.q_offset = d->q_offset;
+    p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split; p.n_work = pl.n_work;
+    p.scale_log2 = d->scale * 1.4426950408889634f;
+    const hipError_t e = ffai::launch_decode(p, mode, ot, d->head_dim, kt, pl.waves, s);
+    if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("decode launch: ") + hipGetErrorString(e));
+    return FFAI_OK;
   }
 
   ffai::FwdParams p{};
@@ -211,21 +290,8 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   p.causal = d->causal; p.q_offset = d->q_offset;
   p.n_qblk = pl.n_qblk; p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split;
   p.n_work = pl.n_work;
-  // The kernels' vector accesses: Q rows 16 B (4 f32 or 8 16-bit elements); K rows and V rows
-  // 16 B in the 16-bit kernels, 4 elements in the f32 kernel; K^T rows 4 keys; O 4 elements.
-  const bool f32 = d->q_dtype == FFAI_F32;
-  const bool kt = d->k_layout == FFAI_K_TRANSPOSED;
-  const int need_q = f32 ? 4 : 8, need_kv = f32 ? 4 : 8, need_k = kt ? 4 : need_kv;
-  p.aligned = vec_of(q, qs, d->q_strides, need_q) == need_q &&
-              vec_of(k, ks, d->k_strides, need_k) == need_k &&
-              vec_of(v, ks, d->v_strides, need_kv) == need_kv &&
-              vec_of(out, os, d->o_strides, 4) == 4;
+  p.aligned = aligned;
   p.scale_log2 = d->scale * 1.4426950408889634f;
-
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int mode = d->q_dtype == FFAI_F32 ? ffai::kF32 : (d->q_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
-  const int kvt = d->kv_dtype == FFAI_F32 ? ffai::kF32 : (d->kv_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
-  const int ot = d->out_dtype == FFAI_F32 ? ffai::kF32 : (d->out_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
   hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt, pl.variant, s);
   if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));
   if (pl.n_split > 1) {
@@ -348,7 +414,7 @@ int ffai_attn_workspace_bytes(const ffai_attn_desc* d, size_t* bytes) {
   const int rc = check_desc(d, &why);
   if (rc == FFAI_DECLINED) return fail(FFAI_DECLINED, "declined: " + why);
   if (rc != FFAI_OK) return fail(rc, why);
-  *bytes = make_plan(d, true).ws_bytes;
+  *bytes = plan_ws_bytes(d);
   return FFAI_OK;
 }
 
@@ -376,7 +442,7 @@ int ffai_attend_workspace_bytes(const ffai_tensor* q, const ffai_tensor* kt, con
   if (attend_accepts(q, kt, v, 0, &why) != FFAI_OK) return fail(FFAI_DECLINED, "declined: " + why);
   ffai_attn_desc d;
   attend_desc(q, kt, v, &d);
-  *bytes = make_plan(&d, true).ws_bytes;
+  *bytes = plan_ws_bytes(&d);
   return FFAI_OK;
 }
 
@@ -426,7 +492,7 @@ int ffai_attend_merged_workspace_bytes(const ffai_tensor* q, const ffai_tensor* 
   if (merged_accepts(q, kt, v, &why) != FFAI_OK) return fail(FFAI_DECLINED, "declined: " + why);
   ffai_attn_desc d;
   merged_desc(q, kt, v, &d);
-  *bytes = make_plan(&d, true).ws_bytes;
+  *bytes = plan_ws_bytes(&d);
   return FFAI_OK;
 }
 

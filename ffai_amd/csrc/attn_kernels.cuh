@@ -26,169 +26,10 @@
 //     workspace and combine_kernel merges them by log-sum-exp.
 #pragma once
 
-#include "attn_kernels.h"
-
-#include <type_traits>
+#include "attn_common.cuh"
 
 namespace ffai {
 namespace {
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-constexpr int BN = kBlockN;
-constexpr float kNegInf = -__builtin_huge_valf();
-// The running max is only raised when a tile's max exceeds it by more than this (log2 units).
-constexpr float kRescaleSlack = 8.0f;
-
-template <int DT>
-using store_t = std::conditional_t<DT == kF32, float, uint16_t>;
-
-// ---------------------------------------------------------------------------------------------
-// Conversions.
-// ---------------------------------------------------------------------------------------------
-template <int DT>
-__device__ __forceinline__ float to_f32(uint32_t bits16) {
-  if constexpr (DT == kBF16) {
-    return __uint_as_float(bits16 << 16);
-  } else {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
-  }
-}
-
-// Two floats to a packed pair (round to nearest even; one v_cvt_pk_* instruction).
-template <int DT>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  const f32x2 x = {lo, hi};
-  if constexpr (DT == kBF16) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
-  } else {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ uint16_t from_f32(float x) {
-  return (uint16_t)(pack2<DT>(x, 0.f) & 0xffffu);
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// The same value from lane l and lane l^32 (v_permlane32_swap): returns {own, partner} in some
-// order, which is all a max or a sum needs.
-__device__ __forceinline__ float partner_max(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float partner_sum(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Element k (0..7) of eight 16-bit values held in a u32x4, paired with the same element of a
-// second row: low half from `r0`, high half from `r1` (one v_perm_b32).
-__device__ __forceinline__ uint32_t pair_elem(u32x4 r0, u32x4 r1, int k) {
-  const uint32_t a = r0[k >> 1], b = r1[k >> 1];
-  return (k & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
-                 : __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-// Same for four 16-bit values held in a u32x2.
-__device__ __forceinline__ uint32_t pair_elem4(u32x2 r0, u32x2 r1, int k) {
-  const uint32_t a = r0[k >> 1], b = r1[k >> 1];
-  return (k & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
-                 : __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-
-// Transposing LDS read (ds_read_b64_tr_b16): see the geometry note at its use.
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x2 lds_tr(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) s16x4* lds_ptr;
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p)));
-}
-
-template <int DT>
-__device__ __forceinline__ f32x16 mfma16(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (DT == kBF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-}
-
-__device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-
-// ---------------------------------------------------------------------------------------------
-// Loads. "vec" loads assume the launch's alignment check passed; "elem" loads take any address.
-// Every helper reads only addresses of valid elements: callers clamp indices into range and
-// zero what is out of range, so no branch (and no wait) splits a tile's loads.
-// ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ u32x2 ld8(const void* p) { return *reinterpret_cast<const u32x2*>(p); }
-
-// 8 consecutive 16-bit elements, element-wise (any alignment).
-__device__ __forceinline__ u32x4 ld8h_elem(const uint16_t* p) {
-  uint32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)p[2 * i] | ((uint32_t)p[2 * i + 1] << 16);
-  return u32x4{w[0], w[1], w[2], w[3]};
-}
-
-// Four elements widened to f32 from f32, f16 or bf16 storage.
-template <int DT, bool VEC>
-__device__ __forceinline__ f32x4 ld4f(const store_t<DT>* p) {
-  if constexpr (DT == kF32) {
-    if constexpr (VEC) return *reinterpret_cast<const f32x4*>(p);
-    return f32x4{p[0], p[1], p[2], p[3]};
-  } else {
-    uint32_t w0, w1;
-    if constexpr (VEC) {
-      const u32x2 a = ld8(p);
-      w0 = a.x;
-      w1 = a.y;
-    } else {
-      w0 = (uint32_t)p[0] | ((uint32_t)p[1] << 16);
-      w1 = (uint32_t)p[2] | ((uint32_t)p[3] << 16);
-    }
-    return f32x4{to_f32<DT>(w0 & 0xffffu), to_f32<DT>(w0 >> 16), to_f32<DT>(w1 & 0xffffu),
-                 to_f32<DT>(w1 >> 16)};
-  }
-}
-
-// Store four consecutive outputs.
-template <int DT, bool VEC>
-__device__ __forceinline__ void st4(store_t<DT>* p, f32x4 x) {
-  if constexpr (DT == kF32) {
-    if constexpr (VEC) {
-      *reinterpret_cast<f32x4*>(p) = x;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = x[e];
-    }
-  } else {
-    const uint32_t a = pack2<DT>(x[0], x[1]), b = pack2<DT>(x[2], x[3]);
-    if constexpr (VEC) {
-      *reinterpret_cast<u32x2*>(p) = u32x2{a, b};
-    } else {
-      p[0] = (uint16_t)(a & 0xffffu);
-      p[1] = (uint16_t)(a >> 16);
-      p[2] = (uint16_t)(b & 0xffffu);
-      p[3] = (uint16_t)(b >> 16);
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------------------------
 // The forward kernel.

@@ -1,5 +1,5 @@
-// Internal interface between the C ABI (attn_api.cpp) and the gfx950 kernels
-// (attn_kernels.hip). Not installed; callers use include/ffai_attn.h.
+// Internal interface between the C ABI (attn_api.cpp) and the gfx950 kernels (attn_launch.hip,
+// fwd_*.hip, decode.hip). Not installed; callers use include/ffai_attn.h.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -31,6 +31,29 @@ struct FwdParams {
   float scale_log2;          // scale * log2(e)
 };
 
+// A decode launch: at most 32 query rows (group x Tq) per (batch, kv-head) unit, operands that
+// admit 16-byte Q/K/V row accesses (8-byte K^T rows) and 4-element output stores.
+struct DecodeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* ws;              // split partials: [B*Hkv][n_split][R][D] O, then [..][R][2] (m, l)
+  const int32_t* kv_lens; // device int32[B] or nullptr
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int32_t B, Hkv, group, Tq, Tk;  // group = Hq / Hkv; rows per unit R = group * Tq <= 32
+  int32_t causal, q_offset;
+  int32_t n_split;          // workgroups per unit
+  int32_t tiles_per_split;  // 64-key tiles per workgroup
+  int32_t n_work;           // B * Hkv * n_split
+  float scale_log2;
+};
+// LDS of decode_combine_kernel (floats): bounds n_split * R * (head_dim + 2).
+constexpr int kCombineLdsFloats = 16384;
+
 struct CombineParams {
   const float* ws;
   void* o;
@@ -61,6 +84,11 @@ hipError_t launch_fwd_f16(const FwdParams& p, int out_dtype, int d, bool kt, int
                           hipStream_t s);
 hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int variant,
                           hipStream_t s);
+
+// The decode kernel with `waves` (4 or 8; 8 only for head_dim 64) waves per workgroup, then the
+// split combine when p.n_split > 1.
+hipError_t launch_decode(const DecodeParams& p, int mode, int out_dtype, int head_dim,
+                         bool k_transposed, int waves, hipStream_t stream);
 
 constexpr int kBlockN = 64;  // keys per tile
 

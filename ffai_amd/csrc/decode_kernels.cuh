@@ -1,0 +1,349 @@
+// gfx950 decode-shaped attention: at most 32 query rows read each K/V head (single-token decode,
+// beams stacked as rows over a shared cross-attention cache, grouped query heads, a few
+// speculative tokens). Memory- and latency-bound, so the design minimises the dependent steps
+// between launch and the last store:
+//   * one workgroup = NWD waves over one (batch, kv-head) and one key range; each wave takes its
+//     own 64-key tiles, so all the tiles' K/V loads are in flight at once and the waves'
+//     softmax/MFMA chains run side by side on the CU's SIMDs;
+//   * the rows of a (batch, kv-head) unit -- every query head of the group and every query
+//     position -- are the 32 columns of one S^T = K Q^T MFMA block, so K and V are read once
+//     per kv-head however many heads or beams share them;
+//   * the waves' partial (O, max, sum) merge through LDS. When one workgroup covers a unit's
+//     keys (decoder self-attention: up to 8 tiles) it writes the output directly; otherwise
+//     each writes its merged partial and decode_combine_kernel, one workgroup per unit, stages
+//     all of a unit's partials in LDS with one round of loads and merges them. (An in-kernel
+//     last-arriver merge needs a device-scope release per workgroup, which on this GPU writes
+//     back the L2 and serialises: measured slower than the second launch.)
+//   * the tile loop is not unrolled: a cold workgroup fetches little code.
+// MFMA operands and fragment layouts are those of fwd_kernel's 16-bit path (attn_kernels.cuh).
+#pragma once
+
+#include "attn_common.cuh"
+
+namespace ffai {
+namespace {
+
+// Output row n (of the unit's R rows), chunk c4 of 4 elements, normalised by l.
+template <int OUTT, int D>
+__device__ __forceinline__ void store_row_chunk(const DecodeParams& p, int b, int hk, int n, int c4,
+                                                f32x4 acc, float l) {
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int h = hk * p.group + n / p.Tq, t = n % p.Tq;
+  store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
+                      (int64_t)t * p.o_st + 4 * c4;
+  st4<OUTT, true>(op, acc * inv);
+}
+
+template <int MODE, int OUTT, int D, bool KT, int NWD>
+__global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
+  static_assert(MODE == kBF16 || MODE == kF16, "decode kernel reads 16-bit Q, K and V");
+  // Per-wave LDS: one K tile ([key][d] or [d][key]) and one V tile ([key][d]), 16-bit.
+  constexpr int KROW = D + 8;
+  constexpr int KTROW = BN + 8;
+  constexpr int VROW = D + 8;
+  constexpr int KBUF = KT ? D * KTROW : BN * KROW;
+  constexpr int VBUF = BN * VROW;
+  constexpr int WBUF = KBUF + VBUF;  // 16-bit elements per wave
+  // After the tiles: per-wave merge area of 32 rows x OROW floats, then 32 maxima, 32 sums.
+  constexpr int OROW = D + 4;
+  constexpr int MBUF = 32 * OROW + 64;
+  static_assert(MBUF * 4 <= WBUF * 2, "the merge area fits in the wave's tile area");
+  static_assert((WBUF * 2) % 16 == 0 && (KBUF * 2) % 16 == 0, "16-byte aligned regions");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NWD * WBUF];
+
+  // ---- which (batch, kv-head, key split): splits of one unit run on one XCD
+  const int hw = blockIdx.x;
+  const int work = (hw & 7) * (int)(gridDim.x >> 3) + (hw >> 3);
+  if (work >= p.n_work) return;
+  const int split = work % p.n_split;
+  const int unit = work / p.n_split;
+  const int hk = unit % p.Hkv;
+  const int b = unit / p.Hkv;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = lane >> 5;
+  const int n32 = lane & 31;  // this lane's query row of the unit (MFMA column)
+  const int R = p.group * p.Tq;
+  const int rn = min(n32, R - 1);
+  const int t_row = rn % p.Tq;
+  const int h_row = hk * p.group + rn / p.Tq;
+
+  int kv_end = p.Tk;
+  if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
+  int kv_blk = kv_end;  // keys any row of the unit may see
+  if (p.causal) kv_blk = min(kv_end, max(0, p.q_offset + p.Tq));
+  const int n_tiles = (kv_blk + BN - 1) / BN;
+  const int t_begin = split * p.tiles_per_split;
+  const int t_end = min(n_tiles, t_begin + p.tiles_per_split);
+  const int iters = t_end > t_begin ? (t_end - t_begin + NWD - 1) / NWD : 0;  // uniform
+  const float sl2 = p.scale_log2;
+  const int lim = p.causal ? min(kv_end - 1, p.q_offset + t_row) : kv_end - 1;
+
+  const uint16_t* kp = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const uint16_t* vp = reinterpret_cast<const uint16_t*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  // ---- Q fragments: B operand of S^T, step s: d = 16s + 8g .. +7 of row rn
+  u32x4 qf[D / 16];
+  {
+    const uint16_t* qr = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_sb + h_row * p.q_sh +
+                         (int64_t)t_row * p.q_st;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      const u32x4 x = ld16(qr + 16 * s + 8 * g);
+      qf[s] = n32 < R ? x : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+  float m_s = kNegInf;  // running max, scaled log2 units (same in lane and lane ^ 32)
+  float l_run = 0.f;    // this lane's half of the running sum
+
+  uint16_t* kl = lds + wave * WBUF;
+  uint16_t* vl = kl + KBUF;
+  const int jt = lane & 15;
+  const int tr_row = jt >> 2, tr_col = 4 * (jt & 3);
+  const int half16 = 16 * ((lane >> 4) & 1);
+
+  // ---- staging (the host launches this kernel only for operands that admit its vector
+  //      accesses). Rows of K and V: 16-byte units, the key index clamped to the last valid key
+  //      and zeroed past it. K^T rows: 4-key (8-byte) chunks, each loaded when all four keys are
+  //      valid and zeroed otherwise; the one chunk per row that straddles the last valid key is
+  //      then patched element by element in LDS. Every address stays inside the operand.
+  auto stage_tile = [&](int it) {
+    const int kb = it * BN;
+    const int klast = kv_end - 1;
+    u32x4 kreg[D / 8], vreg[D / 8];
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) {
+      const int u = lane + 64 * j;
+      if constexpr (KT) {
+        const int d = u / (BN / 8), kc = u % (BN / 8);
+        const int k4 = kb + 8 * kc;
+        const uint16_t* row = kp + (int64_t)d * p.k_st;
+        const bool v0 = k4 + 3 <= klast, v1 = k4 + 7 <= klast;
+        const u32x2 lo = ld8(row + (v0 ? k4 : 0)), hi = ld8(row + (v1 ? k4 + 4 : 0));
+        kreg[j] = u32x4{v0 ? lo.x : 0u, v0 ? lo.y : 0u, v1 ? hi.x : 0u, v1 ? hi.y : 0u};
+      } else {
+        const int key = kb + u / (D / 8), c = u % (D / 8);
+        const u32x4 x = ld16(kp + (int64_t)min(key, klast) * p.k_st + 8 * c);
+        kreg[j] = key <= klast ? x : u32x4{0u, 0u, 0u, 0u};
+      }
+      const int key = kb + u / (D / 8), c = u % (D / 8);
+      const u32x4 x = ld16(vp + (int64_t)min(key, klast) * p.v_st + 8 * c);
+      vreg[j] = key <= klast ? x : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < D / 8; ++j) {
+      const int u = lane + 64 * j;
+      if constexpr (KT) {
+        const int d = u / (BN / 8), kc = u % (BN / 8);
+        *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * kc]) = kreg[j];
+      } else {
+        const int key = u / (D / 8), c = u % (D / 8);
+        *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * c]) = kreg[j];
+      }
+      const int key = u / (D / 8), c = u % (D / 8);
+      *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * c]) = vreg[j];
+    }
+    if constexpr (KT) {
+      const int k4s = klast & ~3;  // the straddling chunk, when the valid keys end inside one
+      if (klast < kb + BN - 1 && (klast & 3) != 3) {
+        for (int d = lane; d < D; d += 64) {
+          const uint16_t* row = kp + (int64_t)d * p.k_st;
+          uint16_t e[3];
+#pragma unroll
+          for (int x = 0; x < 3; ++x) e[x] = row[min(k4s + x, klast)];
+#pragma unroll
+          for (int x = 0; x < 3; ++x)
+            if (k4s + x <= klast) kl[d * KTROW + (k4s - kb) + x] = e[x];
+        }
+      }
+    }
+  };
+
+#pragma unroll 1
+  for (int i = 0; i < iters; ++i) {
+    const int it = t_begin + wave + NWD * i;
+    const bool has = it < t_end;  // wave-uniform
+    const int kb = it * BN;
+    if (i > 0) __syncthreads();  // the previous tile's LDS reads are done
+    if (has) stage_tile(it);
+    __syncthreads();
+    if (!has) continue;
+
+    // ---- S^T for the tile's two 32-key subtiles: sacc[st][r] <-> key kb + 32st + 8(r/4) +
+    //      4g + r%4 of row n32
+    f32x16 sacc[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[st][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) {
+        u32x4 a;
+        if constexpr (KT) {
+          const uint16_t* base = &kl[(16 * s + 8 * g + tr_row) * KTROW + 32 * st + half16 + tr_col];
+          const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
+          a = u32x4{lo.x, lo.y, hi.x, hi.y};
+        } else {
+          a = *reinterpret_cast<const u32x4*>(&kl[(32 * st + n32) * KROW + 16 * s + 8 * g]);
+        }
+        sacc[st] = mfma16<MODE>(a, qf[s], sacc[st]);
+      }
+    }
+    // ---- mask, max, rescale, weights
+    float mx = kNegInf;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + 32 * st + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key > lim) sacc[st][r] = kNegInf;
+        mx = fmaxf(mx, sacc[st][r]);
+      }
+    const float m_new = fmaxf(m_s, partner_max(mx) * sl2);
+    const float corr = (m_new == kNegInf) ? 1.f : fast_exp2(m_s - m_new);
+    m_s = m_new;
+    const float mc = (m_new == kNegInf) ? 0.f : m_new;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= corr;
+    u32x4 pf[4];
+    float rs = 0.f;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float e0 = fast_exp2(__builtin_fmaf(sacc[st][8 * h2 + 2 * k], sl2, -mc));
+          const float e1 = fast_exp2(__builtin_fmaf(sacc[st][8 * h2 + 2 * k + 1], sl2, -mc));
+          const uint32_t pk = pack2<MODE>(e0, e1);
+          w[k] = pk;
+          if constexpr (MODE == kBF16) {
+            rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk),
+                                                 bf16x2{(__bf16)1.f, (__bf16)1.f}, rs, false);
+          } else {
+            rs = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk),
+                                        f16x2{(_Float16)1.f, (_Float16)1.f}, rs, false);
+          }
+        }
+        pf[2 * st + h2] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    l_run = __builtin_fmaf(l_run, corr, rs);
+    // ---- O^T += V^T P^T: 16-key chunk t, A(d = 32dt + n32, keys 16t + 4g + e, 16t + 8 + 4g + e)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const uint16_t* base = &vl[(16 * t + 4 * g + tr_row) * VROW + 32 * dt + half16 + tr_col];
+        const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
+        oacc[dt] = mfma16<MODE>(u32x4{a0.x, a0.y, a1.x, a1.y}, pf[t], oacc[dt]);
+      }
+  }
+
+  // ---- merge the waves' partials through LDS (the tile area is free once all waves pass here)
+  __syncthreads();
+  float* mbase = reinterpret_cast<float*>(lds);
+  {
+    float* mb = mbase + wave * (WBUF / 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<f32x4*>(&mb[n32 * OROW + 32 * dt + 8 * r + 4 * g]) =
+            f32x4{oacc[dt][4 * r], oacc[dt][4 * r + 1], oacc[dt][4 * r + 2], oacc[dt][4 * r + 3]};
+    const float l_tot = partner_sum(l_run);
+    if (g == 0) {
+      mb[32 * OROW + n32] = m_s;
+      mb[32 * OROW + 32 + n32] = l_tot;
+    }
+  }
+  __syncthreads();
+
+  constexpr int C4 = D / 4;  // 4-float chunks per row
+  const int items = R * C4;
+  const int64_t prow0 = ((int64_t)unit * p.n_split + split) * R;  // this split's first partial row
+  float* ws_o = p.ws;
+  float* ws_ml = p.ws + (int64_t)p.B * p.Hkv * p.n_split * R * D;
+
+#pragma unroll 1
+  for (int it = tid; it < items; it += NWD * 64) {
+    const int n = it / C4, c4 = it % C4;
+    float mw[NWD];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NWD; ++w) {
+      mw[w] = mbase[w * (WBUF / 2) + 32 * OROW + n];
+      M = fmaxf(M, mw[w]);
+    }
+    const float Mc = (M == kNegInf) ? 0.f : M;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWD; ++w) {
+      const float* mb = mbase + w * (WBUF / 2);
+      const float wt = fast_exp2(mw[w] - Mc);  // 0 for an empty wave (m = -inf)
+      acc += wt * *reinterpret_cast<const f32x4*>(&mb[n * OROW + 4 * c4]);
+      L = __builtin_fmaf(wt, mb[32 * OROW + 32 + n], L);
+    }
+    if (p.n_split == 1) {
+      store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
+    } else {
+      *reinterpret_cast<f32x4*>(&ws_o[(prow0 + n) * D + 4 * c4]) = acc;
+      if (c4 == 0) *reinterpret_cast<f32x2*>(&ws_ml[(prow0 + n) * 2]) = f32x2{M, L};
+    }
+  }
+}
+
+// Merge a unit's split partials: one workgroup per (batch, kv-head) unit stages every split's
+// (O, m, l) rows in LDS (one round of independent loads), then each thread merges one 4-element
+// chunk of one row by log-sum-exp and writes it. The host keeps n_split * R * (D + 2) floats
+// within kCombineLdsFloats.
+template <int OUTT, int D>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
+  const int unit = blockIdx.x;
+  if (unit >= p.B * p.Hkv) return;
+  const int hk = unit % p.Hkv, b = unit / p.Hkv;
+  const int R = p.group * p.Tq;
+  const int S = p.n_split;
+  __shared__ __attribute__((aligned(16))) float buf[kCombineLdsFloats];
+  const float* so = p.ws + (int64_t)unit * S * R * D;
+  const float* sml = p.ws + (int64_t)p.B * p.Hkv * S * R * D + (int64_t)unit * S * R * 2;
+  const int n_o = S * R * D, n_ml = S * R * 2;
+  const int tid = threadIdx.x;
+  for (int i = 4 * tid; i < n_o; i += 4 * 256)
+    *reinterpret_cast<f32x4*>(&buf[i]) = *reinterpret_cast<const f32x4*>(&so[i]);
+  for (int i = 2 * tid; i < n_ml; i += 2 * 256)
+    *reinterpret_cast<f32x2*>(&buf[n_o + i]) = *reinterpret_cast<const f32x2*>(&sml[i]);
+  __syncthreads();
+  constexpr int C4 = D / 4;
+  const float* ml = buf + n_o;
+#pragma unroll 1
+  for (int it = tid; it < R * C4; it += 256) {
+    const int n = it / C4, c4 = it % C4;
+    float M = kNegInf;
+#pragma unroll 8
+    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[(s * R + n) * 2]);
+    const float Mc = (M == kNegInf) ? 0.f : M;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < S; ++s) {
+      const int row = s * R + n;
+      const float wt = fast_exp2(ml[row * 2] - Mc);
+      acc += wt * *reinterpret_cast<const f32x4*>(&buf[row * D + 4 * c4]);
+      L = __builtin_fmaf(wt, ml[row * 2 + 1], L);
+    }
+    store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
+  }
+}
+
+}  // namespace
+}  // namespace ffai

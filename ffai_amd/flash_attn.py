@@ -166,7 +166,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, k_transposed
               out_dtype: Optional[torch.dtype] = None,
               workspace: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """O = softmax(scale * Q K^T [+ causal mask]) V through ffai_attn_fwd. Returns the output, or
-    None when the descriptor is not served."""
+    None when the descriptor is not served. `workspace` (see workspace_bytes) may be reused by
+    stream-ordered calls and graph replays."""
     lib = L.load()
     if out is None:
         od = out_dtype or (torch.float32 if q.dtype == torch.float32 else q.dtype)

@@ -25,6 +25,11 @@
  * All compute entry points are asynchronous and stream-ordered on `stream` (a hipStream_t;
  * NULL is the device's null stream), allocate no memory, and take device pointers. Distinct
  * streams may be used concurrently from distinct threads. Element strides are in ELEMENTS.
+ *
+ * Workspace: shapes that split the keys over workgroups need a device workspace of
+ * *_workspace_bytes bytes (16-byte aligned) for the partial results; its contents need no
+ * initialisation. A workspace belongs to one call at a time: calls that may overlap (different
+ * streams) need their own; stream-ordered calls and captured HIP graphs may share one.
  */
 #ifndef FFAI_ATTN_H
 #define FFAI_ATTN_H
