@@ -142,8 +142,10 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   SR vreg[V_PER * V_REGS];
 
   // Load tile `it` into kreg/vreg. Interior tiles of an aligned launch take unconditional
-  // vector loads (the uniform `full` branch); tail tiles clamp every index to the last valid key
-  // and zero what lies past it, so they too read only valid addresses without divergent branches.
+  // vector loads (the uniform `full` branch); tail tiles clamp every index to the last valid key,
+  // so they too read only valid addresses without divergent branches. Rows past the last key are
+  // zeroed by store_tile (K^T tails, loaded element-wise, are zeroed here): no value loaded here
+  // is used before the tile is stored.
   auto load_tile = [&](int it) {
     const int kb = it * BN;
     const int klast = kv_end - 1;
@@ -176,8 +178,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         } else {
           const int key = kb + u / (D / 4), c = u % (D / 4);
           const KVS* src = kp + (int64_t)min(key, klast) * p.k_st + 4 * c;
-          const f32x4 x = aligned ? ld4f<KVT, true>(src) : ld4f<KVT, false>(src);
-          kreg[i] = (full || key <= klast) ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+          kreg[i] = aligned ? ld4f<KVT, true>(src) : ld4f<KVT, false>(src);
         }
       } else {
         if constexpr (KT) {
@@ -201,8 +202,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         } else {
           const int key = kb + u / (D / 8), c = u % (D / 8);
           const uint16_t* src = kp + (int64_t)min(key, klast) * p.k_st + 8 * c;
-          const u32x4 x = aligned ? ld16(src) : ld8h_elem(src);
-          kreg[i] = (full || key <= klast) ? x : u32x4{0u, 0u, 0u, 0u};
+          kreg[i] = aligned ? ld16(src) : ld8h_elem(src);
         }
       }
     }
@@ -215,21 +215,25 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         for (int r = 0; r < 4; ++r) {
           const int key = kb + 4 * k4 + r;
           const KVS* src = vp + (int64_t)min(key, klast) * p.v_st + 4 * d4;
-          const f32x4 x = aligned ? ld4f<KVT, true>(src) : ld4f<KVT, false>(src);
-          vreg[4 * i + r] = (full || key <= klast) ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+          vreg[4 * i + r] = aligned ? ld4f<KVT, true>(src) : ld4f<KVT, false>(src);
         }
       } else {
         const int key = kb + u / (D / 8), c = u % (D / 8);
         const uint16_t* src = vp + (int64_t)min(key, klast) * p.v_st + 8 * c;
-        const u32x4 x = aligned ? ld16(src) : ld8h_elem(src);
-        vreg[i] = (full || key <= klast) ? x : u32x4{0u, 0u, 0u, 0u};
+        vreg[i] = aligned ? ld16(src) : ld8h_elem(src);
       }
     }
   };
 
-  auto store_tile = [&](int buf) {
+  // Write the tile `it` held in kreg/vreg to LDS buffer `buf`. Rows past the last valid key
+  // (they were loaded from the clamped address) are zeroed here rather than at load time, so
+  // that nothing waits for the loads until the tile is stored, one iteration later.
+  auto store_tile = [&](int buf, int it) {
     LT* kl = k_lds + buf * KBUF;
     LT* vl = v_lds + buf * VBUF;
+    const int kb = it * BN;
+    const int klast = kv_end - 1;
+    const bool full = kb + BN <= kv_end;
 #pragma unroll
     for (int i = 0; i < K_PER; ++i) {
       const int u = tid + i * NT;
@@ -244,7 +248,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
           }
         } else {
           const int key = u / (D / 4), c = u % (D / 4);
-          *reinterpret_cast<f32x4*>(&kl[key * KROW + 4 * c]) = kreg[i];
+          *reinterpret_cast<f32x4*>(&kl[key * KROW + 4 * c]) =
+              (full || kb + key <= klast) ? kreg[i] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
       } else {
         if constexpr (KT) {
@@ -252,7 +257,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
           *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * kc]) = kreg[i];
         } else {
           const int key = u / (D / 8), c = u % (D / 8);
-          *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * c]) = kreg[i];
+          *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * c]) =
+              (full || kb + key <= klast) ? kreg[i] : u32x4{0u, 0u, 0u, 0u};
         }
       }
     }
@@ -261,15 +267,19 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       const int u = tid + i * NT;
       if constexpr (F32) {
         const int k4 = u / (D / 4), d4 = u % (D / 4);
+        f32x4 rw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          rw[r] = (full || kb + 4 * k4 + r <= klast) ? vreg[4 * i + r] : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const f32x4 col = {vreg[4 * i][c], vreg[4 * i + 1][c], vreg[4 * i + 2][c],
-                             vreg[4 * i + 3][c]};
+          const f32x4 col = {rw[0][c], rw[1][c], rw[2][c], rw[3][c]};
           *reinterpret_cast<f32x4*>(&vl[(4 * d4 + c) * VROW + 4 * k4]) = col;
         }
       } else {
         const int key = u / (D / 8), c = u % (D / 8);
-        *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * c]) = vreg[i];
+        *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * c]) =
+            (full || kb + key <= klast) ? vreg[i] : u32x4{0u, 0u, 0u, 0u};
       }
     }
   };
@@ -293,7 +303,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 
   if (t_begin < t_end) {
     load_tile(t_begin);
-    store_tile(0);
+    store_tile(0, t_begin);
     if (t_begin + 1 < t_end) load_tile(t_begin + 1);
   }
   __syncthreads();
@@ -378,7 +388,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
               oacc[0][dt] = mfma_f32(a[e], sacc[0][st][4 * j + e], oacc[0][dt]);
           }
       if (it + 1 < t_end) {
-        store_tile(buf ^ 1);
+        store_tile(buf ^ 1, it + 1);
         if (it + 2 < t_end) load_tile(it + 2);
       }
       __syncthreads();
@@ -551,7 +561,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       // D
       pv(vl, 1);
       if (it + 1 < t_end) {
-        store_tile(buf ^ 1);
+        store_tile(buf ^ 1, it + 1);
         if (it + 2 < t_end) load_tile(it + 2);
       }
       __syncthreads();
