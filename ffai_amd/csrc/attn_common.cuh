@@ -90,6 +90,24 @@ __device__ __forceinline__ u32x2 lds_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p)));
 }
 
+// 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane l's
+// bytes land at LDS byte address `lds_block` + 16 l. Issued as inline assembly so that the
+// compiler does not wait for it before unrelated LDS reads (it cannot tell which buffer a DMA
+// fills); the caller waits (vm_wait_all) before the barrier that publishes the data. M0 is set
+// here and used by nothing else in these kernels.
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_block) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_block), "v"(src)
+               : "memory", "m0");
+}
+// s_waitcnt vmcnt(0) lgkmcnt(0): every outstanding global load (DMA included) and LDS access done.
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 template <int DT>
 __device__ __forceinline__ f32x16 mfma16(u32x4 a, u32x4 b, f32x16 c) {
   if constexpr (DT == kBF16) {

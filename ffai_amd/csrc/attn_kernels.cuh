@@ -47,19 +47,25 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   using QS = store_t<MODE>;                            // Q global storage type
   static_assert(F32 || KVT == MODE, "16-bit kernels read Q, K and V of one type");
   static_assert(!F32 || QW == 1, "the f32 kernel uses one column block per wave");
-  // LDS tiles, rows padded so that the 128-bit stores and the MFMA operand reads are
-  // bank-conflict free.
-  //   f32:    K [key][d] (KROW = D + 4), V^T [d][key] (VROW = BN + 4) - transposed on the way in.
-  //   16-bit: K [key][d] (KROW = D + 8) when K comes as rows, K^T [d][key] (KTROW = BN + 32) when
-  //           it comes transposed, V [key][d] (VROW = D + 32): all stored as they come, and the
-  //           operands that need the other orientation are read with ds_read_b64_tr_b16.
-  constexpr int KROW = F32 ? D + 4 : D + 8;
-  constexpr int KTROW = BN + 32;
-  constexpr int VROW = F32 ? BN + 4 : D + 32;
+  // LDS tiles.
+  //   f32:    K [key][d] (KROW = D + 4), V^T [d][key] (VROW = BN + 4) - transposed on the way in;
+  //           rows padded so that the 128-bit stores and the operand reads are conflict-free.
+  //   16-bit: K [key][d] when K comes as rows, K^T [d][key] when it comes transposed, V [key][d]:
+  //           all stored as they lie in HBM (so whole tiles go global -> LDS by DMA), the operands
+  //           that need the other orientation read with ds_read_b64_tr_b16. Rows are unpadded;
+  //           instead each row's 16-byte chunks are XOR-permuted (swz_*) so that the fragment
+  //           reads of a wave spread over all banks.
+  constexpr int KROW = F32 ? D + 4 : D;
+  constexpr int KTROW = BN;
+  constexpr int VROW = F32 ? BN + 4 : D;
   constexpr int KBUF = (!F32 && KT) ? D * KTROW : BN * KROW;
   constexpr int VBUF = F32 ? D * VROW : BN * VROW;
-  __shared__ __attribute__((aligned(16))) LT k_lds[2 * KBUF];
-  __shared__ __attribute__((aligned(16))) LT v_lds[2 * VBUF];
+  // f32: double-buffered, one barrier per tile at the tile's end. 16-bit: three buffers, so the
+  // next tile can be staged and published (barrier) before the current tile's last product, and
+  // that product overlaps the next tile's first one.
+  constexpr int NBUF = F32 ? 2 : 3;
+  __shared__ __attribute__((aligned(16))) LT k_lds[NBUF * KBUF];
+  __shared__ __attribute__((aligned(16))) LT v_lds[NBUF * VBUF];
 
   // ---- which (batch, head, query block, key split) this workgroup computes
   const int hw = blockIdx.x;
@@ -140,6 +146,21 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   constexpr int V_REGS = F32 ? 4 : 1;
   SR kreg[K_PER * K_REGS];
   SR vreg[V_PER * V_REGS];
+
+  // 16-bit LDS chunk permutations (chunk = 8 elements = 16 bytes; an XOR, so its own inverse):
+  //   K^T rows (64 keys, 128 B) and 128-byte V rows: the transposing reads of a half-wave touch
+  //   4 consecutive rows x 64 B, rows 2 and 3 land on rows 0 and 1's banks unless their chunks
+  //   are flipped into the other half of the row;
+  //   256-byte V rows (head_dim 128): all rows start on bank 0, so rows r..r+3 take 4 distinct
+  //   64-byte quarters;
+  //   K rows (16-byte reads, one chunk per lane from 32 consecutive rows): even rows 0..14 (and
+  //   odd rows) must hit 8 (16) distinct chunks.
+  auto swz_kt = [](int r, int c) { return c ^ (4 * ((r >> 1) & 1)); };
+  auto swz_v = [](int r, int c) { return D == 64 ? c ^ (4 * ((r >> 1) & 1)) : c ^ (4 * (r & 3)); };
+  auto swz_kr = [](int r, int c) { return D == 64 ? c ^ ((r >> 1) & 7) : c ^ (r & 15); };
+  (void)swz_kt;
+  (void)swz_v;
+  (void)swz_kr;
 
   // Load tile `it` into kreg/vreg. Interior tiles of an aligned launch take unconditional
   // vector loads (the uniform `full` branch); tail tiles clamp every index to the last valid key,
@@ -254,10 +275,10 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       } else {
         if constexpr (KT) {
           const int d = u / (BN / 8), kc = u % (BN / 8);
-          *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * kc]) = kreg[i];
+          *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * swz_kt(d, kc)]) = kreg[i];
         } else {
           const int key = u / (D / 8), c = u % (D / 8);
-          *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * c]) =
+          *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * swz_kr(key, c)]) =
               (full || kb + key <= klast) ? kreg[i] : u32x4{0u, 0u, 0u, 0u};
         }
       }
@@ -278,9 +299,55 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         }
       } else {
         const int key = u / (D / 8), c = u % (D / 8);
-        *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * c]) =
+        *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * swz_v(key, c)]) =
             (full || kb + key <= klast) ? vreg[i] : u32x4{0u, 0u, 0u, 0u};
       }
+    }
+  };
+
+  // 16-bit, full tile of an aligned launch: global -> LDS directly (lds_dma16), one 1024-byte
+  // LDS block (64 chunks) per wave instruction. Lane l of a block fills LDS chunk l, i.e.
+  // physical chunk pc of row r, with the row's logical chunk swz(r, pc). Completion is awaited
+  // (vm_wait_all) before the next workgroup barrier.
+  auto dma_tile = [&](int bufi, int it) {
+    if constexpr (!F32) {
+      const uint32_t kl = lds_addr(k_lds + bufi * KBUF);
+      const uint32_t vl = lds_addr(v_lds + bufi * VBUF);
+      const int kb = it * BN;
+      constexpr int KB = KBUF / 512, VB = VBUF / 512;  // 1024-byte blocks per tile
+      static_assert(KB % NW == 0 && VB % NW == 0, "DMA blocks must tile the workgroup");
+#pragma unroll
+      for (int j = 0; j < KB / NW; ++j) {
+        const int blk = j * NW + wave;
+        const int L = blk * 64 + lane;
+        const uint16_t* src;
+        if constexpr (KT) {
+          const int r = L / (BN / 8), pc = L % (BN / 8);
+          src = kp + (int64_t)r * p.k_st + kb + 8 * swz_kt(r, pc);
+        } else {
+          const int r = L / (D / 8), pc = L % (D / 8);
+          src = kp + (int64_t)(kb + r) * p.k_st + 8 * swz_kr(r, pc);
+        }
+        lds_dma16(src, __builtin_amdgcn_readfirstlane(kl + blk * 1024));
+      }
+#pragma unroll
+      for (int j = 0; j < VB / NW; ++j) {
+        const int blk = j * NW + wave;
+        const int L = blk * 64 + lane;
+        const int r = L / (D / 8), pc = L % (D / 8);
+        const uint16_t* src = vp + (int64_t)(kb + r) * p.v_st + 8 * swz_v(r, pc);
+        lds_dma16(src, __builtin_amdgcn_readfirstlane(vl + blk * 1024));
+      }
+    }
+  };
+  // Stage tile `it` into buffer `bufi`: by DMA when whole and aligned, else through registers
+  // (clamped, zero-filled tail; element-wise loads when misaligned), synchronously.
+  auto stage_tile = [&](int bufi, int it) {
+    if (aligned && it * BN + BN <= kv_end) {
+      dma_tile(bufi, it);
+    } else {
+      load_tile(it);
+      store_tile(bufi, it);
     }
   };
 
@@ -302,9 +369,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   const float sl2 = p.scale_log2;
 
   if (t_begin < t_end) {
-    load_tile(t_begin);
-    store_tile(0, t_begin);
-    if (t_begin + 1 < t_end) load_tile(t_begin + 1);
+    if constexpr (F32) {
+      load_tile(t_begin);
+      store_tile(0, t_begin);
+      if (t_begin + 1 < t_end) load_tile(t_begin + 1);
+    } else {
+      stage_tile(0, t_begin);
+      if (t_begin + 1 < t_end) stage_tile(1, t_begin + 1);
+      vm_wait_all();
+    }
   }
   __syncthreads();
 
@@ -395,12 +468,13 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     }
   } else {
     // ---------------------------------------------------------------------------------------
-    // 16-bit: each 64-key tile runs as four MFMA groups, each interleaved with VALU work that
-    // does not depend on it, so the matrix pipe and the exp/FMA pipe run side by side:
-    //   A  S^T(subtile 0)
+    // 16-bit: each 64-key tile runs as MFMA groups, each interleaved with VALU work that does
+    // not depend on it, so the matrix pipe and the exp/FMA pipe run side by side:
     //   B  S^T(subtile 1)    || max/exp/pack/sum(0)   then rescale O (rare branch)
     //   C  O^T += V^T P^T(0) || max/exp/pack/sum(1)   then rescale O (rare branch)
-    //   D  O^T += V^T P^T(1) then stage the next tile
+    //      stage the next tile into LDS, barrier
+    //   D  O^T += V^T P^T(1) and S^T(subtile 0) of the NEXT tile
+    // so a tile never starts with its operand reads exposed.
     // Probabilities are packed to 16 bits as they are produced; row sums use v_dot2 on the
     // packed pairs, i.e. they sum exactly the weights the second product consumes.
     // ---------------------------------------------------------------------------------------
@@ -417,11 +491,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // A operand of S^T for subtile st, contraction step s: K(key = 32st + n32, d = 16s + 8g + e).
     auto kfrag = [&](const LT* kl, int st, int s) -> u32x4 {
       if constexpr (KT) {
-        const LT* base = &kl[(16 * s + 8 * g + tr_row) * KTROW + 32 * st + half16 + tr_col];
+        // rows r and r + 4 share the chunk permutation (it depends on bit 1 of the row)
+        const int r = 16 * s + 8 * g + tr_row;
+        const int col = 32 * st + half16 + tr_col;
+        const LT* base = &kl[r * KTROW + 8 * swz_kt(r, col >> 3) + (col & 7)];
         const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
         return u32x4{lo.x, lo.y, hi.x, hi.y};
       } else {
-        return *reinterpret_cast<const u32x4*>(&kl[(32 * st + n32) * KROW + 16 * s + 8 * g]);
+        const int r = 32 * st + n32;
+        return *reinterpret_cast<const u32x4*>(&kl[r * KROW + 8 * swz_kr(r, 2 * s + g)]);
       }
     };
     auto qk = [&](f32x16 (&sacc)[QW][2], const LT* kl, int st) {
@@ -504,8 +582,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         const int t = 2 * st + h2;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          // V tile [key][d]: A(d = 32dt + n32, keys 16t + 4g + e (e < 4), 16t + 8 + 4g + e - 4)
-          const LT* base = &vl[(16 * t + 4 * g + tr_row) * VROW + 32 * dt + half16 + tr_col];
+          // V tile [key][d]: A(d = 32dt + n32, keys 16t + 4g + e (e < 4), 16t + 8 + 4g + e - 4);
+          // rows r and r + 8 share the chunk permutation
+          const int r = 16 * t + 4 * g + tr_row;
+          const int col = 32 * dt + half16 + tr_col;
+          const LT* base = &vl[r * VROW + 8 * swz_v(r, col >> 3) + (col & 7)];
           const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
           const u32x4 a = {a0.x, a0.y, a1.x, a1.y};
 #pragma unroll
@@ -514,23 +595,30 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       }
     };
 
-    for (int it = t_begin; it < t_end; ++it) {
-      const int buf = (it - t_begin) & 1;
-      const LT* kl = k_lds + buf * KBUF;
-      const LT* vl = v_lds + buf * VBUF;
+    auto need_mask_of = [&](int it) {
       const int kb = it * BN;
-      const bool need_mask = kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset + q0);
-      f32x16 sacc[QW][2];
+      return kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset + q0);
+    };
+    f32x16 sacc[QW][2];
+    auto zero_sub = [&](int st) {
 #pragma unroll
       for (int c = 0; c < QW; ++c)
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[c][st][r] = 0.f;
-
-      // A
-      qk(sacc, kl, 0);
-      if (need_mask) mask_subtile(sacc, kb, 0);
+        for (int r = 0; r < 16; ++r) sacc[c][st][r] = 0.f;
+    };
+    // S^T of the first tile's subtile 0 (later tiles get theirs in the previous iteration's D)
+    if (t_begin < t_end) {
+      zero_sub(0);
+      qk(sacc, k_lds, 0);
+      if (need_mask_of(t_begin)) mask_subtile(sacc, t_begin * BN, 0);
+    }
+    for (int it = t_begin; it < t_end; ++it) {
+      const int buf = (it - t_begin) % NBUF;
+      const LT* kl = k_lds + buf * KBUF;
+      const LT* vl = v_lds + buf * VBUF;
+      const int kb = it * BN;
+      const bool need_mask = need_mask_of(it);
+      zero_sub(1);
       // B
       __builtin_amdgcn_sched_barrier(0);
       qk(sacc, kl, 1);
@@ -558,13 +646,21 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       pin(1);
       __builtin_amdgcn_sched_barrier(0);
       rescale();
-      // D
-      pv(vl, 1);
-      if (it + 1 < t_end) {
-        store_tile(buf ^ 1, it + 1);
-        if (it + 2 < t_end) load_tile(it + 2);
-      }
+      // Publish tile it + 1 (staged one iteration ago; the barrier also awaits its DMA), then
+      // stage tile it + 2 into the buffer of tile it - 1, which every wave has finished with
+      // once it passes this barrier.
+      const bool more = it + 1 < t_end;
+      const int nbuf = (it + 1 - t_begin) % NBUF;
+      vm_wait_all();
       __syncthreads();
+      if (it + 2 < t_end) stage_tile((it + 2 - t_begin) % NBUF, it + 2);
+      // D: O^T += V^T P^T for subtile 1, and S^T of the next tile's subtile 0
+      pv(vl, 1);
+      if (more) {
+        zero_sub(0);
+        qk(sacc, k_lds + nbuf * KBUF, 0);
+        if (need_mask_of(it + 1)) mask_subtile(sacc, (it + 1) * BN, 0);
+      }
     }
   }
 
