@@ -11,7 +11,8 @@ import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libffai_attn.so")
-HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "ffai_attn.h")
+INCLUDE_DIR = os.path.join(os.path.dirname(HERE), "include")
+HEADER_PATH = os.path.join(INCLUDE_DIR, "ffai_attn.h")
 
 FFAI_OK = 0
 FFAI_DECLINED = 1
@@ -38,6 +39,15 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class KVCacheView(ctypes.Structure):
+    _fields_ = [
+        ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("lens", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32), ("slots", ctypes.c_int32), ("heads", ctypes.c_int32),
+        ("capacity", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+        ("strides", ctypes.c_int64 * 3),
+    ]
+
+
 class TensorView(ctypes.Structure):
     _fields_ = [
         ("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("on_device", ctypes.c_int32),
@@ -57,10 +67,14 @@ class FfaiError(RuntimeError):
 
 
 def header_functions() -> list[str]:
-    """Names of every function include/ffai_attn.h declares."""
-    text = open(HEADER_PATH).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ffai_[a-z0-9_]+)\s*\(", text)))
+    """Names of every function the headers in include/ declare."""
+    names = set()
+    for fn in sorted(os.listdir(INCLUDE_DIR)):
+        if fn.endswith(".h"):
+            text = open(os.path.join(INCLUDE_DIR, fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names |= set(re.findall(r"\b(ffai_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def load():
@@ -92,9 +106,15 @@ def load():
     L.ffai_set_decode_min_keys.argtypes = [ctypes.c_int]
     L.ffai_set_decode_min_keys.restype = None
     L.ffai_attn_last_error.restype = ctypes.c_char_p
+    cp = ctypes.POINTER(KVCacheView)
+    i32, i64 = ctypes.c_int32, ctypes.c_int64
+    L.ffai_kv_append.argtypes = [cp, vp, vp, i32, i32, i64, i64, vp]
+    L.ffai_kv_gather.argtypes = [cp, cp, vp, vp]
+    L.ffai_cross_kv_build.argtypes = [vp, vp, i32, i32, i32, i32, i64, vp, vp, i32, i32, vp]
     for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
-                 "ffai_attend_merged_workspace_bytes"):
+                 "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
+                 "ffai_cross_kv_build"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

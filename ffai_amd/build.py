@@ -1,8 +1,9 @@
 """Build the gfx950 attention library in-tree: ffai_amd/libffai_attn.so.
 
-hipcc compiles the kernel instantiations (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip), the launch
-dispatch (attn_launch.hip) and the C ABI (attn_api.cpp) for gfx950 only, in parallel, then links
-them into one shared library. Packed-FP32 VALU instructions are disabled for all device code.
+hipcc compiles the kernel instantiations (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip, decode.hip),
+the decode-state kernels and their C ABI (kv_cache.hip), the launch dispatch (attn_launch.hip)
+and the attention C ABI (attn_api.cpp) for gfx950 only, in parallel, then links them into one
+shared library. Packed-FP32 VALU instructions are disabled for all device code.
 """
 
 from __future__ import annotations
@@ -18,8 +19,8 @@ ROOT = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "libffai_attn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = [os.path.join(CSRC, n) for n in
-           ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "attn_launch.hip",
-            "attn_api.cpp")]
+           ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "kv_cache.hip",
+            "attn_launch.hip", "attn_api.cpp")]
 ARCH = "gfx950"
 
 

@@ -383,6 +383,13 @@ void merged_desc(const ffai_tensor* q, const ffai_tensor* kt, const ffai_tensor*
 
 }  // namespace
 
+// Shared with the other C-ABI translation units (kv_cache.hip) through attn_kernels.h.
+namespace ffai {
+int api_fail(int code, const char* msg) { return fail(code, msg); }
+void api_clear_error() { g_last_error.clear(); }
+int api_check_device() { return check_device(); }
+}  // namespace ffai
+
 extern "C" {
 
 void ffai_attn_desc_init(ffai_attn_desc* d, int32_t q_dtype, int32_t kv_dtype, int32_t out_dtype,

@@ -90,6 +90,11 @@ hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int 
 hipError_t launch_decode(const DecodeParams& p, int mode, int out_dtype, int head_dim,
                          bool k_transposed, int waves, hipStream_t stream);
 
+// Error and device helpers of the C ABI (attn_api.cpp), for the other entry-point units.
+int api_fail(int code, const char* msg);  // records msg for ffai_attn_last_error, returns code
+void api_clear_error();
+int api_check_device();                   // FFAI_OK, or an error code on a non-gfx950 device
+
 constexpr int kBlockN = 64;  // keys per tile
 
 }  // namespace ffai

@@ -1,0 +1,79 @@
+"""Device-resident decode-step state on torch device tensors, through include/ffai_kv.h.
+
+The reference keeps each decoder layer's self-attention cache as raw (b, L, n_state)
+projections grown by Tensor::cat (crates/ffai-mercury/src/asr/text_decoder.rs:652-662),
+re-splits it into heads every step (:840-842), and snapshots/restores it per beam
+(:1350-1381; decoder.rs:559-583). Here a KVCache holds the head-major layout the attention
+kernels read, appended in place (`append`) and reordered by parent beam (`gather_from`);
+`cross_kv_build` prepares the cross-attention cache once per window (:706-707, :770-773).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+from .flash_attn import _DT, _stream_handle
+
+
+class KVCache:
+    """k, v: (slots, heads, capacity, head_dim) of `dtype`; lens: int32[slots] keys per slot.
+    Attend over it with flash_attn.attention(q, cache.k, cache.v, kv_lens=cache.lens, ...)."""
+
+    def __init__(self, slots: int, heads: int, capacity: int, head_dim: int,
+                 dtype: torch.dtype = torch.bfloat16, device=None):
+        device = device or torch.device("cuda")
+        self.k = torch.zeros(slots, heads, capacity, head_dim, dtype=dtype, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.lens = torch.zeros(slots, dtype=torch.int32, device=device)
+        self.slots, self.heads, self.capacity, self.head_dim = slots, heads, capacity, head_dim
+
+    def view(self) -> L.KVCacheView:
+        c = L.KVCacheView()
+        c.k, c.v, c.lens = self.k.data_ptr(), self.v.data_ptr(), self.lens.data_ptr()
+        c.dtype = _DT[self.k.dtype]
+        c.slots, c.heads, c.capacity, c.head_dim = self.slots, self.heads, self.capacity, self.head_dim
+        for i in range(3):
+            c.strides[i] = self.k.stride(i)
+        return c
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """k_new, v_new: (slots, t, heads * head_dim) projections (f32, f16 or bf16); row t of
+        slot s lands at position lens[s] + t (rows past capacity are dropped)."""
+        assert k_new.shape == v_new.shape and k_new.dim() == 3 and k_new.stride(2) == 1
+        assert v_new.stride() == k_new.stride() and k_new.dtype == v_new.dtype
+        c = self.view()
+        L.check(L.load().ffai_kv_append(ctypes.byref(c), k_new.data_ptr(), v_new.data_ptr(),
+                                        _DT[k_new.dtype], k_new.shape[1], k_new.stride(0),
+                                        k_new.stride(1), _stream_handle(k_new)))
+
+    def gather_from(self, src: "KVCache", parent: torch.Tensor) -> None:
+        """Slot i becomes a copy of src's slot parent[i] (a beam step's reorder)."""
+        assert parent.dtype == torch.int32 and parent.is_cuda and parent.numel() == self.slots
+        d, s = self.view(), src.view()
+        L.check(L.load().ffai_kv_gather(ctypes.byref(d), ctypes.byref(s), parent.data_ptr(),
+                                        _stream_handle(parent)))
+
+
+def cross_kv_build(k_proj: torch.Tensor, v_proj: torch.Tensor, heads: int,
+                   out_dtype: torch.dtype = torch.bfloat16, k_transposed: bool = True,
+                   out: Optional[tuple[torch.Tensor, torch.Tensor]] = None):
+    """k_proj, v_proj: (T, heads * head_dim) -> (K, V) with K (heads, head_dim, T) if
+    k_transposed else (heads, T, head_dim), V (heads, T, head_dim), in out_dtype."""
+    t, n = k_proj.shape
+    assert v_proj.shape == k_proj.shape and k_proj.stride(1) == 1 and v_proj.stride() == k_proj.stride()
+    d = n // heads
+    if out is None:
+        k = torch.empty((heads, d, t) if k_transposed else (heads, t, d), dtype=out_dtype,
+                        device=k_proj.device)
+        v = torch.empty(heads, t, d, dtype=out_dtype, device=k_proj.device)
+    else:
+        k, v = out
+    L.check(L.load().ffai_cross_kv_build(
+        k_proj.data_ptr(), v_proj.data_ptr(), _DT[k_proj.dtype], t, heads, d, k_proj.stride(0),
+        k.data_ptr(), v.data_ptr(), _DT[out_dtype],
+        L.K_TRANSPOSED if k_transposed else L.K_ROWS, _stream_handle(k_proj)))
+    return k, v

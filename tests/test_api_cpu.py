@@ -209,3 +209,53 @@ def test_python_mirror_declines_host_tensors():
     assert fa.attend(q, kt, v) is None
     assert fa.attend_merged(q, kt, v) is None
     assert fa.serves(kt, v) is False
+
+
+# ---------------------------------------------------------------------------------------------
+# decode-state entry points (include/ffai_kv.h): argument checks happen before any HIP call
+# ---------------------------------------------------------------------------------------------
+
+def _cache(dtype=L.BF16, slots=5, heads=16, cap=448, d=64, data=FAKE):
+    c = L.KVCacheView()
+    c.k, c.v, c.lens = data, data + 0x100000, data + 0x200000
+    c.dtype, c.slots, c.heads, c.capacity, c.head_dim = dtype, slots, heads, cap, d
+    c.strides[0], c.strides[1], c.strides[2] = heads * cap * d, cap * d, d
+    return c
+
+
+def test_kv_append_rejects_bad_arguments(lib):
+    c = _cache()
+    ok = dict(src=FAKE, dt=L.F32, t=1, ss=16 * 64, rs=16 * 64)
+
+    def rc(cache=c, **kw):
+        a = {**ok, **kw}
+        return lib.ffai_kv_append(ctypes.byref(cache), a["src"], a["src"], a["dt"], a["t"],
+                                  a["ss"], a["rs"], None)
+
+    assert rc(dt=7) == L.FFAI_ERR_INVALID
+    assert rc(src=None) == L.FFAI_ERR_INVALID
+    assert rc(t=-1) == L.FFAI_ERR_INVALID
+    assert rc(rs=10) == L.FFAI_ERR_INVALID          # shorter than heads * head_dim
+    assert rc(cache=_cache(d=60)) == L.FFAI_ERR_INVALID  # head_dim not a multiple of 8
+    assert rc(cache=_cache(data=0)) == L.FFAI_ERR_INVALID
+    assert rc(t=0) == L.FFAI_OK                      # nothing to do, nothing launched
+
+
+def test_kv_gather_rejects_bad_arguments(lib):
+    a, b = _cache(), _cache(data=FAKE + 0x1000000)
+    assert lib.ffai_kv_gather(ctypes.byref(a), ctypes.byref(a), FAKE, None) == L.FFAI_ERR_INVALID
+    assert lib.ffai_kv_gather(ctypes.byref(a), ctypes.byref(b), None, None) == L.FFAI_ERR_INVALID
+    c = _cache(dtype=L.F16, data=FAKE + 0x2000000)
+    assert lib.ffai_kv_gather(ctypes.byref(a), ctypes.byref(c), FAKE, None) == L.FFAI_ERR_INVALID
+    assert "dtype" in L.last_error()
+
+
+def test_cross_kv_build_rejects_bad_arguments(lib):
+    def rc(t=1500, heads=16, d=64, rs=1024, layout=L.K_TRANSPOSED, odt=L.BF16):
+        return lib.ffai_cross_kv_build(FAKE, FAKE, L.F32, t, heads, d, rs, FAKE, FAKE, odt, layout,
+                                       None)
+    assert rc(t=0) == L.FFAI_ERR_INVALID
+    assert rc(d=256) == L.FFAI_ERR_INVALID
+    assert rc(rs=1000) == L.FFAI_ERR_INVALID
+    assert rc(layout=9) == L.FFAI_ERR_INVALID
+    assert rc(odt=5) == L.FFAI_ERR_INVALID
