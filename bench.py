@@ -8,13 +8,15 @@ calls. FLOP = 4 * B * H * T^2 * D per layer (flash_probe.rs:432's convention).
 
 Also reported: the beam-5 decode step at the whisper-medium shape (24 layers of decoder
 self-attention over ragged per-beam caches plus cross-attention over 1500 shared encoder frames,
-bf16 K/V, f32 output), the whisper-tiny f32 and whisper-small bf16 encoders, the
+bf16 K/V, f32 output), the device-resident decode state of that step (K/V append in place and
+beam reorder, with and without the attention calls, and the per-window cross-attention cache
+build), the whisper-tiny f32 and whisper-small bf16 encoders, the
 Qwen2-VL-2B-shape causal prefill (12 query heads over 2 K/V heads, head_dim 128, S = 4096), and
 the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this host's cores on a
 bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras]
-                       [--layers L] [--legs decode,tiny,small,prefill | none | copy]
+                       [--layers L] [--legs decode,state,tiny,small,prefill | none | copy]
 """
 
 from __future__ import annotations
@@ -41,9 +43,9 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--legs", default="decode,tiny,small,prefill",
+    ap.add_argument("--legs", default="decode,state,tiny,small,prefill",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
+                         "state, tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
                          "calibration used to scale HBM byte counters")
     return ap.parse_args()
 
@@ -226,6 +228,130 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
 
 
 # ------------------------------------------------------------------------------------------
+# Device-resident decode state (whisper-medium: 24 layers, beam 5, 16 heads, D=64)
+# ------------------------------------------------------------------------------------------
+
+def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=448,
+                       layers=24, mid_len=224):
+    """A beam step's state work on the device: per layer, append this step's K/V row of every
+    beam (f32 projections -> bf16 cache), then reorder the beams of all layers by parent into
+    the other cache of a ping-pong pair in one launch; then the same step with the attention calls between append and reorder
+    (self-attention over the beams' caches, cross-attention over the window's shared cache).
+    All beams of a step share one length, as in beam search; lengths start so that the timed
+    steps are centred on `mid_len`. Also times the per-window cross-attention cache build of
+    the 24 layers (f32 projections -> bf16 K^T and V)."""
+    from ffai_amd.kv_cache import KVCache, cross_kv_build
+
+    dev = torch.device("cuda:0")
+    gd = torch.Generator(device=dev).manual_seed(3)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    scale = D ** -0.5
+    bf = torch.bfloat16
+    total = warmup + steps
+    start_len = max(1, mid_len - total // 2)
+    assert start_len + total <= cap
+    caches = [KVCache(beams, H, cap, D, bf, dev, layers=layers) for _ in range(2)]
+    caches[0].k.normal_(generator=gd)
+    caches[0].v.normal_(generator=gd)
+    projs, xs = [], []
+    for _ in range(layers):
+        projs.append((torch.randn(beams, 1, H * D, generator=gd, device=dev),
+                      torch.randn(beams, 1, H * D, generator=gd, device=dev),
+                      torch.randn(beams, H, 1, D, generator=gd, device=dev).to(bf),
+                      torch.randn(beams, H, 1, D, generator=gd, device=dev).to(bf)))
+        kp = torch.randn(T_enc, H * D, generator=gd, device=dev)
+        vp = torch.randn(T_enc, H * D, generator=gd, device=dev)
+        xs.append((kp, vp) + cross_kv_build(kp, vp, H, bf, k_transposed=True))
+    parent = torch.randint(0, beams, (beams,), generator=g, dtype=torch.int32).to(dev)
+    o_self = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
+    o_x = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
+    q0, k0 = projs[0][2], caches[0].layer(0)
+    ws_self = torch.empty(max(1, fa.workspace_bytes(q0, k0.k, k0.v, o_self, scale=scale,
+                                                    kv_lens=k0.lens)), dtype=torch.uint8, device=dev)
+    ws_x = torch.empty(max(1, fa.workspace_bytes(projs[0][3].permute(2, 1, 0, 3), xs[0][2][None],
+                                                 xs[0][3][None], o_x.permute(2, 1, 0, 3),
+                                                 k_transposed=True, scale=scale)),
+                       dtype=torch.uint8, device=dev)
+
+    def step(phase, attend):
+        cur, nxt = caches[phase], caches[1 - phase]
+        for l in range(layers):
+            c = cur.layer(l)
+            nk, nv, qs, qx = projs[l]
+            c.append(nk, nv)
+            if attend:
+                fa.attention(qs, c.k, c.v, scale=scale, kv_lens=c.lens, out=o_self,
+                             workspace=ws_self)
+                fa.attention(qx.permute(2, 1, 0, 3), xs[l][2][None], xs[l][3][None],
+                             k_transposed=True, scale=scale, out=o_x.permute(2, 1, 0, 3),
+                             workspace=ws_x)
+        nxt.gather_from(cur, parent)   # every layer's reorder in one launch
+
+    def timed(attend):
+        caches[0].lens.fill_(start_len)
+        torch.cuda.synchronize()
+        graphs = []
+        for phase in (0, 1):   # capture does not execute: the lengths stay at start_len
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step(phase, attend)
+            graphs.append(gr)
+        torch.cuda.synchronize()
+        for i in range(warmup):
+            graphs[i % 2].replay()
+        stream = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(warmup, total):
+            graphs[i % 2].replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        final = int(caches[total % 2].lens[0, 0])
+        assert final == start_len + total, (final, start_len, total)
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    us_state = timed(False)
+    us_full = timed(True)
+    # algorithmic bytes of the state work per step (lengths after the append, averaged over
+    # the timed steps): append reads the f32 rows and writes bf16; the reorder reads and
+    # writes every beam's valid prefix of K and V
+    mean_len = start_len + warmup + (steps + 1) / 2.0
+    row = H * D
+    append_bytes = layers * beams * 2 * row * (4 + 2)
+    gather_bytes = layers * beams * 2 * row * 2 * 2 * mean_len
+    state_bytes = append_bytes + gather_bytes
+    # per-window cross cache build, all layers
+    reps = 20
+
+    def build_all():
+        for kp, vp, kx, vx in xs:
+            cross_kv_build(kp, vp, H, bf, k_transposed=True, out=(kx, vx))
+
+    build_all()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        build_all()
+    e1.record()
+    torch.cuda.synchronize()
+    us_build = e0.elapsed_time(e1) * 1e3 / reps
+    build_bytes = layers * 2 * T_enc * row * (4 + 2)
+    return {
+        "state_us_per_step": us_state,
+        "state_bytes_per_step": state_bytes,
+        "state_gbps": state_bytes / (us_state * 1e-6) / 1e9,
+        "full_step_us": us_full,
+        "mean_self_len": mean_len,
+        "cross_build_us_per_window": us_build,
+        "cross_build_gbps": build_bytes / (us_build * 1e-6) / 1e9,
+        "launches_per_step": layers + 1,
+    }
+
+
+# ------------------------------------------------------------------------------------------
 # CPU baseline: the oracle (reference algorithm restated) on this host's cores
 # ------------------------------------------------------------------------------------------
 
@@ -310,6 +436,12 @@ def main():
         dec = decode_bench(torch, fa, max(args.steps * 10, 100), 10)
         log(f"decode: {dec['us_per_step']:.1f} us/step, {dec['gbps']:.0f} GB/s")
         extras["decode_beam5"] = dec
+    if "state" in legs:
+        log("decode state: append + beam reorder, whisper-medium ...")
+        st = decode_state_bench(torch, fa, 100, 10)
+        log(f"decode state: {st['state_us_per_step']:.1f} us/step ({st['state_gbps']:.0f} GB/s), "
+            f"full step {st['full_step_us']:.1f} us, cross build {st['cross_build_us_per_window']:.1f} us")
+        extras["decode_state_beam5"] = st
     if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")
         tiny = encoder_bench(torch, fa, max(args.steps * 5, 50), args.warmup, 4, B=1, H=6,

@@ -109,7 +109,7 @@ def load():
     cp = ctypes.POINTER(KVCacheView)
     i32, i64 = ctypes.c_int32, ctypes.c_int64
     L.ffai_kv_append.argtypes = [cp, vp, vp, i32, i32, i64, i64, vp]
-    L.ffai_kv_gather.argtypes = [cp, cp, vp, vp]
+    L.ffai_kv_gather.argtypes = [cp, cp, vp, i32, i64, i64, vp]
     L.ffai_cross_kv_build.argtypes = [vp, vp, i32, i32, i32, i32, i64, vp, vp, i32, i32, vp]
     for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <type_traits>
 
 #include "attn_common.cuh"
 
@@ -113,45 +114,79 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
 }
 
 struct GatherParams {
-  void* dk;
-  void* dv;
+  char* dk;
+  char* dv;
   int32_t* dlens;
-  const void* sk;
-  const void* sv;
+  const char* sk;
+  const char* sv;
   const int32_t* slens;
   const int32_t* parent;
-  int64_t ds, dh, dp;  // destination slot, head, position strides
-  int64_t ss, sh, sp;  // source strides
-  int32_t src_slots, heads, head_dim, capacity, n_blk;
+  int64_t ds, dh, dp;  // destination slot, head, position strides (bytes)
+  int64_t ss, sh, sp;  // source strides (bytes)
+  int64_t layer_stride, lens_layer_stride;  // bytes between layers' k/v; ints between lens
+  int32_t src_slots, heads, capacity, n_blk;
+  int32_t row_units;   // units per key row (16 bytes each when vec, else one element)
   int32_t vec;
 };
 
-// Workgroup (slot i, head h, 64-position block): copies the block if it holds any of the parent's
-// keys. Parent indices and lengths are clamped into range, so no access leaves either cache.
-template <int DT>
+// Workgroup (layer blockIdx.y; slot i, head h, 64-position block): copies the block if it holds
+// any of the parent's keys. The caches have one dtype, so rows move as raw bytes: 16-byte units
+// when every row start is 16-byte aligned, else one element (ES bytes) at a time. Each thread
+// issues all its loads before its stores. Parent indices and lengths are clamped into range, so
+// no access leaves either cache.
+template <int ES>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
+  using elem_t = std::conditional_t<ES == 4, uint32_t, uint16_t>;
+  constexpr int kPer = 4;  // units per thread per pass, for K and for V
   const int blk = blockIdx.x % p.n_blk;
   const int h = (blockIdx.x / p.n_blk) % p.heads;
   const int i = blockIdx.x / (p.n_blk * p.heads);
+  const int64_t lo = (int64_t)blockIdx.y * p.layer_stride;
+  const int32_t* slens = p.slens + (int64_t)blockIdx.y * p.lens_layer_stride;
   const int par = min(max(p.parent[i], 0), p.src_slots - 1);
-  const int len = min(max(p.slens[par], 0), p.capacity);
-  if (blk == 0 && h == 0 && threadIdx.x == 0) p.dlens[i] = len;
+  const int len = min(max(slens[par], 0), p.capacity);
+  if (blk == 0 && h == 0 && threadIdx.x == 0)
+    p.dlens[(int64_t)blockIdx.y * p.lens_layer_stride + i] = len;
   const int pos0 = blk * 64;
   if (pos0 >= len) return;
-  const int rows = min(64, len - pos0);
-  const int row_units = p.head_dim / 8;
-  const auto* sk = reinterpret_cast<const store_t<DT>*>(p.sk) + (int64_t)par * p.ss + (int64_t)h * p.sh;
-  const auto* sv = reinterpret_cast<const store_t<DT>*>(p.sv) + (int64_t)par * p.ss + (int64_t)h * p.sh;
-  auto* dk = reinterpret_cast<store_t<DT>*>(p.dk) + (int64_t)i * p.ds + (int64_t)h * p.dh;
-  auto* dv = reinterpret_cast<store_t<DT>*>(p.dv) + (int64_t)i * p.ds + (int64_t)h * p.dh;
-  for (int u = threadIdx.x; u < rows * row_units; u += 256) {
-    const int r = u / row_units, d = (u - r * row_units) * 8;
-    const int pos = pos0 + r;
-    float x[8];
-    load8<DT>(sk + (int64_t)pos * p.sp + d, p.vec, x);
-    store8<DT>(dk + (int64_t)pos * p.dp + d, p.vec, x);
-    load8<DT>(sv + (int64_t)pos * p.sp + d, p.vec, x);
-    store8<DT>(dv + (int64_t)pos * p.dp + d, p.vec, x);
+  const int n = min(64, len - pos0) * p.row_units;
+  const char* sk = p.sk + lo + (int64_t)par * p.ss + (int64_t)h * p.sh + (int64_t)pos0 * p.sp;
+  const char* sv = p.sv + lo + (int64_t)par * p.ss + (int64_t)h * p.sh + (int64_t)pos0 * p.sp;
+  char* dk = p.dk + lo + (int64_t)i * p.ds + (int64_t)h * p.dh + (int64_t)pos0 * p.dp;
+  char* dv = p.dv + lo + (int64_t)i * p.ds + (int64_t)h * p.dh + (int64_t)pos0 * p.dp;
+  const int ub = p.vec ? 16 : ES;  // bytes per unit
+  for (int base = threadIdx.x; base < n; base += 256 * kPer) {
+    if (p.vec) {
+      u32x4 a[kPer], b[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int u = base + j * 256;
+        if (u < n) {
+          const int r = u / p.row_units, c = (u - r * p.row_units) * ub;
+          a[j] = *reinterpret_cast<const u32x4*>(sk + r * p.sp + c);
+          b[j] = *reinterpret_cast<const u32x4*>(sv + r * p.sp + c);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int u = base + j * 256;
+        if (u < n) {
+          const int r = u / p.row_units, c = (u - r * p.row_units) * ub;
+          *reinterpret_cast<u32x4*>(dk + r * p.dp + c) = a[j];
+          *reinterpret_cast<u32x4*>(dv + r * p.dp + c) = b[j];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int u = base + j * 256;
+        if (u < n) {
+          const int r = u / p.row_units, c = (u - r * p.row_units) * ub;
+          *reinterpret_cast<elem_t*>(dk + r * p.dp + c) = *reinterpret_cast<const elem_t*>(sk + r * p.sp + c);
+          *reinterpret_cast<elem_t*>(dv + r * p.dp + c) = *reinterpret_cast<const elem_t*>(sv + r * p.sp + c);
+        }
+      }
+    }
   }
 }
 
@@ -310,7 +345,7 @@ int ffai_kv_append(const ffai_kv_cache* c, const void* new_k, const void* new_v,
 }
 
 int ffai_kv_gather(const ffai_kv_cache* dst, const ffai_kv_cache* src, const int32_t* parent,
-                   void* stream) {
+                   int32_t layers, int64_t layer_stride, int64_t lens_layer_stride, void* stream) {
   api_clear_error();
   int rc = check_cache(dst);
   if (rc != FFAI_OK) return rc;
@@ -322,24 +357,30 @@ int ffai_kv_gather(const ffai_kv_cache* dst, const ffai_kv_cache* src, const int
     return api_fail(FFAI_ERR_INVALID, "dst and src differ in dtype, heads, head_dim or capacity");
   if (dst->k == src->k || dst->v == src->v || dst->lens == src->lens)
     return api_fail(FFAI_ERR_INVALID, "dst and src must be distinct caches");
+  if (layers < 1 || layers > 65535) return api_fail(FFAI_ERR_INVALID, "layers must be in [1, 65535]");
+  if (layers > 1 && (layer_stride <= 0 || lens_layer_stride < dst->slots || lens_layer_stride < src->slots))
+    return api_fail(FFAI_ERR_INVALID, "layer strides must separate the layers");
+  if (layers == 1) layer_stride = lens_layer_stride = 0;
   rc = api_check_device();
   if (rc != FFAI_OK) return rc;
+  const int64_t es = (int64_t)esize(dt_of(dst->dtype));
   GatherParams p{};
-  p.dk = dst->k; p.dv = dst->v; p.dlens = dst->lens;
-  p.sk = src->k; p.sv = src->v; p.slens = src->lens; p.parent = parent;
-  p.ds = dst->strides[0]; p.dh = dst->strides[1]; p.dp = dst->strides[2];
-  p.ss = src->strides[0]; p.sh = src->strides[1]; p.sp = src->strides[2];
-  p.src_slots = src->slots; p.heads = dst->heads; p.head_dim = dst->head_dim;
+  p.dk = static_cast<char*>(dst->k); p.dv = static_cast<char*>(dst->v); p.dlens = dst->lens;
+  p.sk = static_cast<const char*>(src->k); p.sv = static_cast<const char*>(src->v);
+  p.slens = src->lens; p.parent = parent;
+  p.ds = dst->strides[0] * es; p.dh = dst->strides[1] * es; p.dp = dst->strides[2] * es;
+  p.ss = src->strides[0] * es; p.sh = src->strides[1] * es; p.sp = src->strides[2] * es;
+  p.layer_stride = layer_stride * es; p.lens_layer_stride = lens_layer_stride;
+  p.src_slots = src->slots; p.heads = dst->heads;
   p.capacity = dst->capacity; p.n_blk = (dst->capacity + 63) / 64;
-  const size_t es = esize(dt_of(dst->dtype));
-  p.vec = aligned8(dst->k, es, {p.ds, p.dh, p.dp}) && aligned8(dst->v, es, {0}) &&
-          aligned8(src->k, es, {p.ss, p.sh, p.sp}) && aligned8(src->v, es, {0});
-  const dim3 grid((unsigned)((int64_t)dst->slots * dst->heads * p.n_blk));
+  p.vec = aligned8(dst->k, es, {dst->strides[0], dst->strides[1], dst->strides[2], layer_stride}) &&
+          aligned8(dst->v, es, {0}) && aligned8(src->k, es, {src->strides[0], src->strides[1], src->strides[2]}) &&
+          aligned8(src->v, es, {0}) && (dst->head_dim * es) % 16 == 0;
+  p.row_units = p.vec ? (int32_t)(dst->head_dim * es / 16) : dst->head_dim;
+  const dim3 grid((unsigned)((int64_t)dst->slots * dst->heads * p.n_blk), (unsigned)layers);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int dt = dt_of(dst->dtype);
-  if (dt == kF32) hipLaunchKernelGGL((kv_gather_kernel<kF32>), grid, dim3(256), 0, st, p);
-  else if (dt == kF16) hipLaunchKernelGGL((kv_gather_kernel<kF16>), grid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((kv_gather_kernel<kBF16>), grid, dim3(256), 0, st, p);
+  if (es == 4) hipLaunchKernelGGL((kv_gather_kernel<4>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((kv_gather_kernel<2>), grid, dim3(256), 0, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
   return FFAI_OK;

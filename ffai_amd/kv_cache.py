@@ -21,28 +21,46 @@ from .flash_attn import _DT, _stream_handle
 
 class KVCache:
     """k, v: (slots, heads, capacity, head_dim) of `dtype`; lens: int32[slots] keys per slot.
-    Attend over it with flash_attn.attention(q, cache.k, cache.v, kv_lens=cache.lens, ...)."""
+    Attend over it with flash_attn.attention(q, cache.k, cache.v, kv_lens=cache.lens, ...).
+
+    With `layers`, the cache holds a decoder's whole stack: k, v are (layers, slots, heads,
+    capacity, head_dim) and lens (layers, slots); `layer(l)` is layer l's cache (a view), which
+    is appended and attended per layer, while `gather_from` reorders every layer in one launch."""
 
     def __init__(self, slots: int, heads: int, capacity: int, head_dim: int,
-                 dtype: torch.dtype = torch.bfloat16, device=None):
-        device = device or torch.device("cuda")
-        self.k = torch.zeros(slots, heads, capacity, head_dim, dtype=dtype, device=device)
-        self.v = torch.zeros_like(self.k)
-        self.lens = torch.zeros(slots, dtype=torch.int32, device=device)
+                 dtype: torch.dtype = torch.bfloat16, device=None, layers: Optional[int] = None,
+                 _views=None):
+        if _views is not None:
+            self.k, self.v, self.lens = _views
+        else:
+            device = device or torch.device("cuda")
+            lead = (layers,) if layers is not None else ()
+            self.k = torch.zeros(*lead, slots, heads, capacity, head_dim, dtype=dtype, device=device)
+            self.v = torch.zeros_like(self.k)
+            self.lens = torch.zeros(*lead, slots, dtype=torch.int32, device=device)
+        self.layers = layers
         self.slots, self.heads, self.capacity, self.head_dim = slots, heads, capacity, head_dim
 
+    def layer(self, l: int) -> "KVCache":
+        assert self.layers is not None and 0 <= l < self.layers
+        return KVCache(self.slots, self.heads, self.capacity, self.head_dim,
+                       _views=(self.k[l], self.v[l], self.lens[l]))
+
     def view(self) -> L.KVCacheView:
+        """The C descriptor of this cache (of layer 0 for a layer stack)."""
+        k = self.k[0] if self.layers is not None else self.k
         c = L.KVCacheView()
         c.k, c.v, c.lens = self.k.data_ptr(), self.v.data_ptr(), self.lens.data_ptr()
         c.dtype = _DT[self.k.dtype]
         c.slots, c.heads, c.capacity, c.head_dim = self.slots, self.heads, self.capacity, self.head_dim
         for i in range(3):
-            c.strides[i] = self.k.stride(i)
+            c.strides[i] = k.stride(i)
         return c
 
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """k_new, v_new: (slots, t, heads * head_dim) projections (f32, f16 or bf16); row t of
         slot s lands at position lens[s] + t (rows past capacity are dropped)."""
+        assert self.layers is None, "append to one layer: cache.layer(l).append(...)"
         assert k_new.shape == v_new.shape and k_new.dim() == 3 and k_new.stride(2) == 1
         assert v_new.stride() == k_new.stride() and k_new.dtype == v_new.dtype
         c = self.view()
@@ -51,11 +69,17 @@ class KVCache:
                                         k_new.stride(1), _stream_handle(k_new)))
 
     def gather_from(self, src: "KVCache", parent: torch.Tensor) -> None:
-        """Slot i becomes a copy of src's slot parent[i] (a beam step's reorder)."""
+        """Slot i becomes a copy of src's slot parent[i] (a beam step's reorder), in every layer."""
         assert parent.dtype == torch.int32 and parent.is_cuda and parent.numel() == self.slots
+        assert self.layers == src.layers
+        layers, ls, lls = 1, 0, 0
+        if self.layers is not None:
+            assert self.k.stride(0) == src.k.stride(0) == self.v.stride(0) == src.v.stride(0)
+            assert self.lens.stride(0) == src.lens.stride(0)
+            layers, ls, lls = self.layers, self.k.stride(0), self.lens.stride(0)
         d, s = self.view(), src.view()
         L.check(L.load().ffai_kv_gather(ctypes.byref(d), ctypes.byref(s), parent.data_ptr(),
-                                        _stream_handle(parent)))
+                                        layers, ls, lls, _stream_handle(parent)))
 
 
 def cross_kv_build(k_proj: torch.Tensor, v_proj: torch.Tensor, heads: int,

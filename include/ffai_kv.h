@@ -58,12 +58,16 @@ int ffai_kv_append(const ffai_kv_cache* c, const void* new_k, const void* new_v,
                    int32_t t_new, int64_t src_slot_stride, int64_t src_row_stride, void* stream);
 
 /* Beam reorder: slot i of dst becomes a copy of slot parent[i] of src (its first
- * src.lens[parent[i]] positions) and dst.lens[i] = src.lens[parent[i]]. parent is a device
- * int32[dst.slots] of values in [0, src.slots). dst and src must be distinct caches of the same
- * dtype, heads, head_dim and capacity (callers alternate two). Replaces the per-beam
- * DecoderState restore of decode_beam (decoder.rs:559-583, text_decoder.rs:1350-1381). */
+ * src.lens[parent[i]] positions) and dst.lens[i] = src.lens[parent[i]], in each of `layers`
+ * decoder layers at once. dst and src describe layer 0; layer l's k and v start layer_stride
+ * elements after layer l-1's (in both caches) and its lens lens_layer_stride ints after
+ * (>= slots); with layers == 1 both strides are ignored. parent is a device int32[dst.slots] of
+ * values in [0, src.slots), shared by all layers. dst and src must be distinct caches of the
+ * same dtype, heads, head_dim and capacity (callers alternate two). One launch per beam step
+ * replaces the per-beam DecoderState restore of every layer (decoder.rs:559-583,
+ * text_decoder.rs:1350-1381). */
 int ffai_kv_gather(const ffai_kv_cache* dst, const ffai_kv_cache* src, const int32_t* parent,
-                   void* stream);
+                   int32_t layers, int64_t layer_stride, int64_t lens_layer_stride, void* stream);
 
 /* Cross-attention cache build: k_proj and v_proj are (t, heads * head_dim) row-major (row stride
  * src_row_stride) projections of the encoder output; writes v_out as (heads, t, head_dim) and

@@ -243,11 +243,19 @@ def test_kv_append_rejects_bad_arguments(lib):
 
 def test_kv_gather_rejects_bad_arguments(lib):
     a, b = _cache(), _cache(data=FAKE + 0x1000000)
-    assert lib.ffai_kv_gather(ctypes.byref(a), ctypes.byref(a), FAKE, None) == L.FFAI_ERR_INVALID
-    assert lib.ffai_kv_gather(ctypes.byref(a), ctypes.byref(b), None, None) == L.FFAI_ERR_INVALID
-    c = _cache(dtype=L.F16, data=FAKE + 0x2000000)
-    assert lib.ffai_kv_gather(ctypes.byref(a), ctypes.byref(c), FAKE, None) == L.FFAI_ERR_INVALID
+
+    def rc(dst=a, src=b, parent=FAKE, layers=1, ls=0, lls=0):
+        return lib.ffai_kv_gather(ctypes.byref(dst), ctypes.byref(src), parent, layers, ls, lls,
+                                  None)
+
+    assert rc(src=a) == L.FFAI_ERR_INVALID           # in place
+    assert rc(parent=None) == L.FFAI_ERR_INVALID
+    assert rc(src=_cache(dtype=L.F16, data=FAKE + 0x2000000)) == L.FFAI_ERR_INVALID
     assert "dtype" in L.last_error()
+    assert rc(layers=0) == L.FFAI_ERR_INVALID
+    assert rc(layers=24, ls=0, lls=5) == L.FFAI_ERR_INVALID   # layers would overlap
+    assert rc(layers=24, ls=1 << 20, lls=2) == L.FFAI_ERR_INVALID  # lens rows overlap
+    assert "layer strides" in L.last_error()
 
 
 def test_cross_kv_build_rejects_bad_arguments(lib):

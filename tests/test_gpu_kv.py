@@ -77,6 +77,46 @@ def test_gather_follows_parents(gpu):
         assert torch.equal(dst.v[i, :, :n], src.v[p, :, :n])
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_layered_gather_follows_parents(gpu, dtype, aligned):
+    """One launch reorders a 3-layer stack whose layers hold different lengths. The unaligned
+    case views caches whose rows start 2 elements into padded rows (row stride head_dim + 4),
+    which takes the element-wise copy."""
+    rng = np.random.default_rng(15)
+    layers, slots, heads, d, cap = 3, 5, 4, 64, 100
+    lens = np.array([[5, 100, 64, 65, 1], [0, 7, 99, 3, 50], [100, 100, 100, 100, 100]], np.int32)
+    parent = np.array([3, 3, 0, 4, 1], np.int32)
+    tdt = TDT[dtype]
+
+    def make():
+        if aligned:
+            return KVCache(slots, heads, cap, d, tdt, gpu, layers=layers)
+        pad_k = torch.zeros(layers, slots, heads, cap, d + 4, dtype=tdt, device=gpu)
+        pad_v = torch.zeros_like(pad_k)
+        lens_t = torch.zeros(layers, slots, dtype=torch.int32, device=gpu)
+        c = KVCache(slots, heads, cap, d, layers=layers,
+                    _views=(pad_k[..., 2:2 + d], pad_v[..., 2:2 + d], lens_t))
+        c._pads = (pad_k, pad_v)
+        return c
+
+    src, dst = make(), make()
+    src.k.copy_(torch.from_numpy(randn(rng, src.k.shape)))
+    src.v.copy_(torch.from_numpy(randn(rng, src.v.shape)))
+    src.lens.copy_(torch.from_numpy(lens))
+    dst.gather_from(src, torch.from_numpy(parent).to(gpu))
+    np.testing.assert_array_equal(dst.lens.cpu().numpy(), lens[:, parent])
+    for l in range(layers):
+        for i, p in enumerate(parent.tolist()):
+            n = int(lens[l, p])
+            assert torch.equal(dst.k[l, i, :, :n], src.k[l, p, :, :n]), (l, i)
+            assert torch.equal(dst.v[l, i, :, :n], src.v[l, p, :, :n]), (l, i)
+            # positions past the parent's length are left alone
+            assert not dst.k[l, i, :, n:].any()
+    if not aligned:  # the padding around each row is untouched
+        assert not dst._pads[0][..., :2].any() and not dst._pads[0][..., 2 + d:].any()
+
+
 @pytest.mark.parametrize("k_transposed", [True, False])
 @pytest.mark.parametrize("out", ["bf16", "f16"])
 def test_cross_cache_build(gpu, k_transposed, out):
