@@ -22,6 +22,9 @@ constexpr int BN = kBlockN;
 constexpr float kNegInf = -__builtin_huge_valf();
 // The running max is only raised when a tile's max exceeds it by more than this (log2 units).
 constexpr float kRescaleSlack = 8.0f;
+// 16-bit encoder kernel: a lane's sum of 16 weights above this (2^64) sends the subtile to the
+// exact-max path, so no weight exceeds it.
+constexpr float kWeightSumBound = 18446744073709551616.0f;
 
 template <int DT>
 using store_t = std::conditional_t<DT == kF32, float, uint16_t>;

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps q0 scalar
   const int g = lane >> 5;    // lane group: which half of each MFMA contraction step
   const int n32 = lane & 31;  // query column of the accumulators
   constexpr int BM = NW * 32 * QW;
@@ -480,8 +480,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // ---------------------------------------------------------------------------------------
     constexpr int NQK = (D / 16) * QW;        // MFMAs per subtile in S^T
     constexpr int NPV = 2 * (D / 32) * QW;    // MFMAs per subtile in O^T
-    constexpr int EXPO_VALU = QW * 72;        // VALU instructions of one max/exp/pack/sum step
     u32x4 pf[QW][4];   // packed P: pf[c][t] = keys 16t..16t+15 of the tile, B-operand order
+    f32x16 sacc[QW][2];  // S^T of the tile's two 32-key subtiles, per column block
 
     // Transposing-read geometry: in each 16-lane group, lane j reads 4 elements of row
     // (r0 + j/4) at column (c0 + 4*(j%4)); lane j then holds column c0 + j of rows r0..r0+3.
@@ -510,23 +510,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         for (int c = 0; c < QW; ++c) sacc[c][st] = mfma16<MODE>(a, qf[c][s], sacc[c][st]);
       }
     };
-    float corr_s[QW];  // accumulator rescale owed by the last max update of column block c
-    // Weights of column block c, subtile st, from its 16 scores `sv`. The running max is raised
-    // without a branch, and lazily: only when a score exceeds it by more than kRescaleSlack
-    // (log2 units), so the weights stay below 2^kRescaleSlack and the rescale the accumulator
-    // then owes (corr_s) is rare. The row sum takes the rescale at once; the accumulator takes
-    // it in `rescale`, after the products that used the previous weights were issued.
-    auto expo_c = [&](const f32x16& sv, int c, int st) {
-      float mx = kNegInf;
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sv[r], sv[r + 1]));
-      const float mx_s = partner_max(mx) * sl2;
-      const float m_old = m_s[c];
-      const float m_new = (mx_s > m_old + kRescaleSlack) ? mx_s : m_old;
-      const float corr = (m_new == m_old) ? 1.f : fast_exp2(m_old - m_new);
-      m_s[c] = m_new;
-      corr_s[c] = corr;
-      const float mc = (m_new == kNegInf) ? 0.f : m_new;
+    float corr_s[QW];  // accumulator rescale owed by the last update of column block c's max
+    float rs_s[QW];    // this lane's sum of the weights of the subtile just exponentiated
+    // Weights of column block c, subtile st, from its 16 scores `sv` against the reference max
+    // mc (scaled log2 units), packed to 16 bits into pf; returns this lane's sum of the packed
+    // weights (v_dot2 on the packed pairs: exactly the weights the second product consumes).
+    auto exps_c = [&](const f32x16& sv, int c, int st, float mc) -> float {
       float rs = 0.f;
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
@@ -549,11 +538,68 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         }
         pf[c][2 * st + h2] = u32x4{w[0], w[1], w[2], w[3]};
       }
-      l_run[c] = __builtin_fmaf(l_run[c], corr, rs);
+      return rs;
     };
-    auto expo = [&](f32x16 (&sacc)[QW][2], int st) {
+    // Fast path, inside the phase: weights against the current reference max m_s, with no max
+    // taken. m_s starts as the row max of the first subtile (set before the loop) and never
+    // exceeds the true running max, so the largest weight of a row is >= 1 and nothing that
+    // matters underflows; it is raised only in `settle`, when a subtile's weights leave the
+    // range below. Work unit: pair k (scores 2k, 2k+1) of column block c of subtile st.
+    constexpr int NPAIR = QW * 8;  // pairs per subtile
+    uint32_t pw[QW][8];            // packed pairs of the subtile being exponentiated
+    auto exp_pair = [&](int st, int pidx) {
+      const int c = pidx >> 3, k = pidx & 7;
+      const float mc = m_s[c];
+      const float e0 = fast_exp2(__builtin_fmaf(sacc[c][st][2 * k], sl2, -mc));
+      const float e1 = fast_exp2(__builtin_fmaf(sacc[c][st][2 * k + 1], sl2, -mc));
+      const uint32_t pk = pack2<MODE>(e0, e1);
+      pw[c][k] = pk;
+      if constexpr (MODE == kBF16) {
+        rs_s[c] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk),
+                                                  bf16x2{(__bf16)1.f, (__bf16)1.f}, rs_s[c], false);
+      } else {
+        rs_s[c] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk),
+                                         f16x2{(_Float16)1.f, (_Float16)1.f}, rs_s[c], false);
+      }
+    };
+    auto publish_pairs = [&](int st) {
 #pragma unroll
-      for (int c = 0; c < QW; ++c) expo_c(sacc[c][st], c, st);
+      for (int c = 0; c < QW; ++c) {
+        pf[c][2 * st] = u32x4{pw[c][0], pw[c][1], pw[c][2], pw[c][3]};
+        pf[c][2 * st + 1] = u32x4{pw[c][4], pw[c][5], pw[c][6], pw[c][7]};
+      }
+    };
+    // After the phase: a lane sum above kWeightSumBound (so some weight may be), or inf/NaN (a
+    // score far above m_s, or m_s still -inf because every key so far was masked), makes the
+    // whole wave redo that subtile against the subtile's exact row max (rare: with N(0,1)-like
+    // scores only the first tile of a row can take it). Every weight therefore stays at most
+    // 2^64, and the row sums and accumulators stay finite in f32 for any realistic key count.
+    // The test compares bit patterns: the build assumes no NaNs, so a float compare could be
+    // folded.
+    auto settle = [&](int st) {
+      bool bad = false;
+#pragma unroll
+      for (int c = 0; c < QW; ++c) {
+        corr_s[c] = 1.f;
+        bad = bad || (__float_as_uint(rs_s[c]) & 0x7fffffffu) > __float_as_uint(kWeightSumBound);
+      }
+      if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+#pragma unroll
+        for (int c = 0; c < QW; ++c) {
+          const f32x16& sv = sacc[c][st];
+          float mx = kNegInf;
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sv[r], sv[r + 1]));
+          const float mx_s = partner_max(mx) * sl2;
+          const float m_old = m_s[c];
+          const float m_new = fmaxf(m_old, mx_s);
+          corr_s[c] = (m_new == m_old) ? 1.f : fast_exp2(m_old - m_new);
+          m_s[c] = m_new;
+          rs_s[c] = exps_c(sv, c, st, (m_new == kNegInf) ? 0.f : m_new);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < QW; ++c) l_run[c] = __builtin_fmaf(l_run[c], corr_s[c], rs_s[c]);
     };
     // Apply the owed rescale to the accumulator (whole wave, only when some row owes one).
     auto rescale = [&]() {
@@ -565,15 +611,6 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         for (int c = 0; c < QW; ++c)
 #pragma unroll
           for (int dt = 0; dt < D / 32; ++dt) oacc[c][dt] *= corr_s[c];
-      }
-    };
-    // Keep the exp/pack/sum work of subtile `st` inside the phase that hides it: without a use
-    // here, LLVM sinks it next to its consumer, past the phase's end.
-    auto pin = [&](int st) {
-#pragma unroll
-      for (int c = 0; c < QW; ++c) {
-        asm volatile("" : "+v"(pf[c][2 * st]), "+v"(pf[c][2 * st + 1]), "+v"(l_run[c]),
-                     "+v"(corr_s[c]));
       }
     };
     auto pv = [&](const LT* vl, int st) {
@@ -595,11 +632,62 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       }
     };
 
+    // The two phases that hide the exp work. Each issues its fragment reads first, then its
+    // MFMAs one at a time, each followed by an equal share of the exp/pack/sum pairs of the
+    // other subtile, fenced so that the compiler keeps that order: one wave then keeps the
+    // matrix pipe and the VALU busy together instead of issuing its MFMAs back to back.
+    //   B: S^T(subtile 1) || exps(subtile 0);   C: O^T += V^T P^T(subtile 0) || exps(subtile 1)
+    auto phase_b = [&](const LT* kl) {
+      u32x4 a[D / 16];
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) a[s] = kfrag(kl, 1, s);
+#pragma unroll
+      for (int c = 0; c < QW; ++c) rs_s[c] = 0.f;
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) {
+        const int s = i / QW, c = i % QW;
+        sacc[c][1] = mfma16<MODE>(a[s], qf[c][s], sacc[c][1]);
+#pragma unroll
+        for (int j = i * NPAIR / NQK; j < (i + 1) * NPAIR / NQK; ++j) exp_pair(0, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      publish_pairs(0);
+    };
+    auto vfrag = [&](const LT* vl, int t, int dt) -> u32x4 {
+      // V tile [key][d]: A(d = 32dt + n32, keys 16t + 4g + e (e < 4), 16t + 8 + 4g + e - 4);
+      // rows r and r + 8 share the chunk permutation
+      const int r = 16 * t + 4 * g + tr_row;
+      const int col = 32 * dt + half16 + tr_col;
+      const LT* base = &vl[r * VROW + 8 * swz_v(r, col >> 3) + (col & 7)];
+      const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
+      return u32x4{a0.x, a0.y, a1.x, a1.y};
+    };
+    auto phase_c = [&](const LT* vl) {
+      u32x4 a[2][D / 32];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt) a[h2][dt] = vfrag(vl, h2, dt);
+#pragma unroll
+      for (int c = 0; c < QW; ++c) rs_s[c] = 0.f;
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        const int h2 = i / (QW * (D / 32)), dt = (i / QW) % (D / 32), c = i % QW;
+        oacc[c][dt] = mfma16<MODE>(a[h2][dt], pf[c][h2], oacc[c][dt]);
+#pragma unroll
+        for (int j = i * NPAIR / NPV; j < (i + 1) * NPAIR / NPV; ++j) exp_pair(1, j);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      publish_pairs(1);
+    };
+
+    // wave-uniform, and made visibly so, so that masking is a scalar branch rather than
+    // predicated selects on every tile
     auto need_mask_of = [&](int it) {
       const int kb = it * BN;
-      return kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset + q0);
+      return __builtin_amdgcn_readfirstlane(kb + BN > kv_end ||
+                                            (p.causal && kb + BN - 1 > p.q_offset + q0)) != 0;
     };
-    f32x16 sacc[QW][2];
     auto zero_sub = [&](int st) {
 #pragma unroll
       for (int c = 0; c < QW; ++c)
@@ -611,6 +699,14 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       zero_sub(0);
       qk(sacc, k_lds, 0);
       if (need_mask_of(t_begin)) mask_subtile(sacc, t_begin * BN, 0);
+      // the reference max: this subtile's row max (-inf if all of it is masked)
+#pragma unroll
+      for (int c = 0; c < QW; ++c) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[c][0][r], sacc[c][0][r + 1]));
+        m_s[c] = partner_max(mx) * sl2;
+      }
     }
     for (int it = t_begin; it < t_end; ++it) {
       const int buf = (it - t_begin) % NBUF;
@@ -621,30 +717,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       zero_sub(1);
       // B
       __builtin_amdgcn_sched_barrier(0);
-      qk(sacc, kl, 1);
-      expo(sacc, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, D / 16, 0);  // K fragment reads first
-#pragma unroll
-      for (int i = 0; i < NQK; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, EXPO_VALU / NQK, 0);  // then VALU
-      }
-      pin(0);
+      phase_b(kl);
       __builtin_amdgcn_sched_barrier(0);
+      settle(0);
       rescale();
       if (need_mask) mask_subtile(sacc, kb, 1);
       // C
       __builtin_amdgcn_sched_barrier(0);
-      pv(vl, 0);
-      expo(sacc, 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, D / 16, 0);  // V fragment reads first
-#pragma unroll
-      for (int i = 0; i < NPV; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, EXPO_VALU / NPV, 0);
-      }
-      pin(1);
+      phase_c(vl);
       __builtin_amdgcn_sched_barrier(0);
+      settle(1);
       rescale();
       // Publish tile it + 1 (staged one iteration ago; the barrier also awaits its DMA), then
       // stage tile it + 2 into the buffer of tile it - 1, which every wave has finished with

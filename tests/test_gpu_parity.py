@@ -120,6 +120,37 @@ def test_encoder_16bit(gpu, dtype, k_transposed, out_f32):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k_transposed", [True, False])
+def test_scores_far_above_the_first_subtile(gpu, dtype, k_transposed):
+    """The 16-bit kernel takes its reference max from each row's first 32 keys and raises it
+    only when a subtile's weights would leave [0, 2^64]. Scores here jump twice: by ~58 log2
+    units at keys 200-259 (weights near 2^58, accepted as they are) and by ~173 at keys 640-699
+    (weights past f32's range, so that subtile is redone against its exact max and the
+    accumulator rescaled). Without the redo the second jump gives inf and then NaN."""
+    rng = np.random.default_rng(77)
+    b, h, t, d = 1, 2, 1000, 64
+    rnd = round_bf16 if dtype == torch.bfloat16 else round_f16
+    u = np.zeros(d, np.float32)
+    u[3] = 1.0
+    q = rnd(8.0 * u + 0.05 * randn(rng, (b, h, t, d)))
+    amp = np.full(t, 0.1, np.float32)
+    amp[200:260] = 40.0
+    amp[640:700] = 120.0
+    k = rnd(amp[None, None, :, None] * u + 0.05 * randn(rng, (b, h, t, d)))
+    v = rnd(randn(rng, (b, h, t, d)))
+    scale = 0.125
+    kk = np.ascontiguousarray(np.swapaxes(k, 2, 3)) if k_transposed else k
+    out = fa.attention(_dev(q, dtype, gpu), _dev(kk, dtype, gpu), _dev(v, dtype, gpu),
+                       k_transposed=k_transposed, scale=scale, out_dtype=torch.float32)
+    got = _host(out)
+    assert np.isfinite(got).all()
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=scale)
+    err = max_abs(got, want)
+    print(f"score jumps {dtype} kt={k_transposed}: {err:.3e}")
+    assert err < TOL_BF16
+
+
 def test_encoder_f32_batched_rows_layout(gpu):
     rng = np.random.default_rng(3)
     b, h, t, d = 2, 2, 700, 64
