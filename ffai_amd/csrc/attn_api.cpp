@@ -291,6 +291,13 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   p.n_qblk = pl.n_qblk; p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split;
   p.n_work = pl.n_work;
   p.aligned = aligned;
+  {
+    // the DMA path addresses a tile's rows by 32-bit byte offsets from the tile's first key
+    const int64_t k_rows = kt ? d->head_dim : ffai::kBlockN;
+    const int64_t lim = int64_t(1) << 31;
+    p.dma = aligned && !f32 && k_rows * d->k_strides[2] * 2 < lim &&
+            int64_t(ffai::kBlockN) * d->v_strides[2] * 2 < lim;
+  }
   p.scale_log2 = d->scale * 1.4426950408889634f;
   hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt, pl.variant, s);
   if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));

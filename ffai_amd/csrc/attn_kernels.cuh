@@ -6,20 +6,23 @@
 //     (32 keys x 32 queries per v_mfma_f32_32x32x16_{bf16,f16} / 32x32x2_f32). In the 32x32
 //     accumulator layout lane l owns query column l%32 and 16 of the 32 keys, lane l^32 the
 //     other 16, so every softmax statistic (row max, row sum, rescale factor) is a per-lane
-//     scalar; the only cross-lane step is one v_permlane32_swap per tile for the row max.
+//     scalar; the only cross-lane step is a v_permlane32_swap when a row max is taken.
 //   * The probabilities stay in registers: the accumulator of S^T is already the B operand
 //     of O^T = V^T P^T once the key order inside each 16-key MFMA step is permuted the same
 //     way on both operands (the contraction is a sum, so any shared order is exact).
 //   * With QW = 2 a wave computes two 32-query column blocks against each K/V fragment it
 //     reads from LDS, halving LDS operand traffic per FLOP (at 32 queries per wave the LDS
 //     read bandwidth alone would cap the MFMA pipes near 80 %).
-//   * K and V tiles are staged through double-buffered LDS once per workgroup: K as rows
-//     [key][d] (A operand of the first product), V transposed [d][key] (A operand of the
-//     second). The reference's K^T layout and V's row layout are transposed on the way in with
-//     register permutes. Global loads run two tiles ahead; one barrier per tile.
-//   * Online softmax in base 2 with v_exp_f32. The running max only moves when a tile's max
-//     exceeds it by more than 2^8 in probability (the weights then stay below 256, exact in f32
-//     and bf16 alike), so after the first tile the accumulator rescale is almost never paid.
+//   * K and V tiles are staged through LDS once per workgroup. f32: double-buffered, K as rows
+//     and V transposed, permuted in registers on the way in. 16-bit: three buffers filled by
+//     global->LDS DMA in the layout they have in HBM (K^T or K rows, V rows), read back with
+//     transposing LDS reads where an operand needs the other orientation. One barrier per tile.
+//   * Online softmax in base 2 with v_exp_f32. f32 kernel: the running max only moves when a
+//     tile's max exceeds it by more than 2^8 in probability. 16-bit kernels: no max is taken on
+//     the common path at all. Each row's reference max is the max of its first 32 keys, and
+//     weights are computed against it directly. A subtile whose weights would exceed 2^64 (or
+//     overflow) is redone against its exact max, with the accumulator rescaled; that is rare
+//     for real scores, and it keeps every weight and sum finite in f32.
 //   * Workgroup ids are remapped so that all query blocks of one (batch, kv-head) run on the
 //     same XCD (the hardware deals workgroup i to XCD i % 8) and share that XCD's L2.
 //   * Few-query shapes (decode) split the keys over workgroups; partial (O, m, l) go to the
@@ -91,6 +94,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 
   int kv_end = p.Tk;
   if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
+  kv_end = __builtin_amdgcn_readfirstlane(kv_end);  // uniform (one batch item per workgroup)
   int kv_blk = kv_end;  // keys any row of this workgroup may see
   if (p.causal) kv_blk = min(kv_end, max(0, p.q_offset + min(qb * BM + BM, p.Tq)));
   const int n_tiles = (kv_blk + BN - 1) / BN;
@@ -309,41 +313,51 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   // LDS block (64 chunks) per wave instruction. Lane l of a block fills LDS chunk l, i.e.
   // physical chunk pc of row r, with the row's logical chunk swz(r, pc). Completion is awaited
   // (vm_wait_all) before the next workgroup barrier.
+  // DMA geometry: each thread moves KB/NW 16-byte chunks of the K tile and VB/NW of the V tile
+  // per tile; its byte offsets from the tile's first key (the XOR chunk permutation included)
+  // are the same for every tile, so they are computed once and each tile only moves the
+  // wave-uniform base.
+  constexpr int KB_ = (!F32) ? KBUF / 512 : NW, VB_ = (!F32) ? VBUF / 512 : NW;  // 1 KB blocks
+  uint32_t dma_koff[KB_ / NW], dma_voff[VB_ / NW];
+  if constexpr (!F32) {
+    static_assert(KB_ % NW == 0 && VB_ % NW == 0, "DMA blocks must tile the workgroup");
+#pragma unroll
+    for (int j = 0; j < KB_ / NW; ++j) {
+      const int L = (j * NW + wave) * 64 + lane;
+      if constexpr (KT) {
+        const int r = L / (BN / 8), pc = L % (BN / 8);
+        dma_koff[j] = (uint32_t)(2 * ((int64_t)r * p.k_st + 8 * swz_kt(r, pc)));
+      } else {
+        const int r = L / (D / 8), pc = L % (D / 8);
+        dma_koff[j] = (uint32_t)(2 * ((int64_t)r * p.k_st + 8 * swz_kr(r, pc)));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VB_ / NW; ++j) {
+      const int L = (j * NW + wave) * 64 + lane;
+      const int r = L / (D / 8), pc = L % (D / 8);
+      dma_voff[j] = (uint32_t)(2 * ((int64_t)r * p.v_st + 8 * swz_v(r, pc)));
+    }
+  }
   auto dma_tile = [&](int bufi, int it) {
     if constexpr (!F32) {
       const uint32_t kl = lds_addr(k_lds + bufi * KBUF);
       const uint32_t vl = lds_addr(v_lds + bufi * VBUF);
-      const int kb = it * BN;
-      constexpr int KB = KBUF / 512, VB = VBUF / 512;  // 1024-byte blocks per tile
-      static_assert(KB % NW == 0 && VB % NW == 0, "DMA blocks must tile the workgroup");
+      const int64_t kb = (int64_t)it * BN;
+      const char* kbase = reinterpret_cast<const char*>(kp + (KT ? kb : kb * p.k_st));
+      const char* vbase = reinterpret_cast<const char*>(vp + kb * p.v_st);
 #pragma unroll
-      for (int j = 0; j < KB / NW; ++j) {
-        const int blk = j * NW + wave;
-        const int L = blk * 64 + lane;
-        const uint16_t* src;
-        if constexpr (KT) {
-          const int r = L / (BN / 8), pc = L % (BN / 8);
-          src = kp + (int64_t)r * p.k_st + kb + 8 * swz_kt(r, pc);
-        } else {
-          const int r = L / (D / 8), pc = L % (D / 8);
-          src = kp + (int64_t)(kb + r) * p.k_st + 8 * swz_kr(r, pc);
-        }
-        lds_dma16(src, __builtin_amdgcn_readfirstlane(kl + blk * 1024));
-      }
+      for (int j = 0; j < KB_ / NW; ++j)
+        lds_dma16_sbase(kbase, dma_koff[j], kl + (j * NW + wave) * 1024);
 #pragma unroll
-      for (int j = 0; j < VB / NW; ++j) {
-        const int blk = j * NW + wave;
-        const int L = blk * 64 + lane;
-        const int r = L / (D / 8), pc = L % (D / 8);
-        const uint16_t* src = vp + (int64_t)(kb + r) * p.v_st + 8 * swz_v(r, pc);
-        lds_dma16(src, __builtin_amdgcn_readfirstlane(vl + blk * 1024));
-      }
+      for (int j = 0; j < VB_ / NW; ++j)
+        lds_dma16_sbase(vbase, dma_voff[j], vl + (j * NW + wave) * 1024);
     }
   };
   // Stage tile `it` into buffer `bufi`: by DMA when whole and aligned, else through registers
   // (clamped, zero-filled tail; element-wise loads when misaligned), synchronously.
   auto stage_tile = [&](int bufi, int it) {
-    if (aligned && it * BN + BN <= kv_end) {
+    if (p.dma && it * BN + BN <= kv_end) {
       dma_tile(bufi, it);
     } else {
       load_tile(it);
@@ -470,8 +484,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // ---------------------------------------------------------------------------------------
     // 16-bit: each 64-key tile runs as MFMA groups, each interleaved with VALU work that does
     // not depend on it, so the matrix pipe and the exp/FMA pipe run side by side:
-    //   B  S^T(subtile 1)    || max/exp/pack/sum(0)   then rescale O (rare branch)
-    //   C  O^T += V^T P^T(0) || max/exp/pack/sum(1)   then rescale O (rare branch)
+    //   B  S^T(subtile 1)    || exp/pack/sum(0)   then the rare redo and rescale
+    //   C  O^T += V^T P^T(0) || exp/pack/sum(1)   then the rare redo and rescale
     //      stage the next tile into LDS, barrier
     //   D  O^T += V^T P^T(1) and S^T(subtile 0) of the NEXT tile
     // so a tile never starts with its operand reads exposed.
@@ -510,8 +524,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         for (int c = 0; c < QW; ++c) sacc[c][st] = mfma16<MODE>(a, qf[c][s], sacc[c][st]);
       }
     };
-    float corr_s[QW];  // accumulator rescale owed by the last update of column block c's max
     float rs_s[QW];    // this lane's sum of the weights of the subtile just exponentiated
+    float corr_s[QW];  // accumulator rescale owed by the last redo of column block c
     // Weights of column block c, subtile st, from its 16 scores `sv` against the reference max
     // mc (scaled log2 units), packed to 16 bits into pf; returns this lane's sum of the packed
     // weights (v_dot2 on the packed pairs: exactly the weights the second product consumes).
@@ -601,7 +615,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 #pragma unroll
       for (int c = 0; c < QW; ++c) l_run[c] = __builtin_fmaf(l_run[c], corr_s[c], rs_s[c]);
     };
-    // Apply the owed rescale to the accumulator (whole wave, only when some row owes one).
+    // Apply the rescale a redo left owing to the accumulator (whole wave, rare). Kept apart from
+    // `settle`: inside its branch the accumulator would need copies on the common path.
     auto rescale = [&]() {
       bool any = false;
 #pragma unroll
@@ -646,9 +661,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 #pragma unroll
       for (int i = 0; i < NQK; ++i) {
         const int s = i / QW, c = i % QW;
-        sacc[c][1] = mfma16<MODE>(a[s], qf[c][s], sacc[c][1]);
 #pragma unroll
         for (int j = i * NPAIR / NQK; j < (i + 1) * NPAIR / NQK; ++j) exp_pair(0, j);
+        sacc[c][1] = mfma16<MODE>(a[s], qf[c][s], sacc[c][1]);
         __builtin_amdgcn_sched_barrier(0);
       }
       publish_pairs(0);
@@ -673,9 +688,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 #pragma unroll
       for (int i = 0; i < NPV; ++i) {
         const int h2 = i / (QW * (D / 32)), dt = (i / QW) % (D / 32), c = i % QW;
-        oacc[c][dt] = mfma16<MODE>(a[h2][dt], pf[c][h2], oacc[c][dt]);
 #pragma unroll
         for (int j = i * NPAIR / NPV; j < (i + 1) * NPAIR / NPV; ++j) exp_pair(1, j);
+        oacc[c][dt] = mfma16<MODE>(a[h2][dt], pf[c][h2], oacc[c][dt]);
         __builtin_amdgcn_sched_barrier(0);
       }
       publish_pairs(1);

@@ -28,6 +28,8 @@ struct FwdParams {
   int32_t tiles_per_split;   // key tiles (of 64) per split
   int32_t n_work;            // B * Hq * n_qblk * n_split logical workgroups
   int32_t aligned;           // every operand admits the kernels' vector loads and stores
+  int32_t dma;               // 16-bit: whole tiles may go global -> LDS by DMA (aligned, and
+                             // each lane's byte offset within a K or V tile fits 32 bits)
   float scale_log2;          // scale * log2(e)
 };
 

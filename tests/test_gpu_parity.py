@@ -151,6 +151,44 @@ def test_scores_far_above_the_first_subtile(gpu, dtype, k_transposed):
     assert err < TOL_BF16
 
 
+def _views_with_high_low_word(gpu, arrays, dtype):
+    """Device copies of `arrays` placed in one buffer at an address whose low 32 bits have bit
+    31 set (the DMA path builds its 64-bit scalar base from two 32-bit halves)."""
+    esz = torch.tensor([], dtype=dtype).element_size()
+    sizes = [((a.size * esz + 255) // 256) * 256 for a in arrays]
+    buf = torch.empty(2 ** 31 + sum(sizes) + 4096, dtype=torch.uint8, device=gpu)
+    lo = buf.data_ptr() & 0xFFFFFFFF
+    off = 0 if lo >= 2 ** 31 else ((2 ** 31 - lo + 255) // 256) * 256
+    out = []
+    for a, n in zip(arrays, sizes):
+        t = buf[off:off + a.size * esz].view(dtype).view(a.shape)
+        t.copy_(torch.from_numpy(np.ascontiguousarray(a)).to(dtype))
+        assert t.data_ptr() & 0x80000000
+        out.append(t)
+        off += n
+    return buf, out
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 300), (8, 16, 512)])
+def test_operands_at_high_addresses(gpu, shape):
+    """Regression: operands whose addresses have bit 31 of the low word set, through the
+    one-wave (B2 H3 T300) and the 4-wave x 2-block (B8 H16 T512) encoder variants."""
+    rng = np.random.default_rng(31)
+    b, h, t = shape
+    d = 64
+    q = round_bf16(randn(rng, (b, h, t, d)))
+    kt = round_bf16(randn(rng, (b, h, d, t)))
+    v = round_bf16(randn(rng, (b, h, t, d)))
+    buf, (qd, ktd, vd) = _views_with_high_low_word(gpu, [q, kt, v], torch.bfloat16)
+    out = fa.attention(qd, ktd, vd, k_transposed=True, scale=0.125, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    del buf
+    want = oracle.attend_general(q, kt, v, k_transposed=True, scale=0.125)
+    err = max_abs(_host(out), want)
+    print(f"high addresses {shape}: {err:.3e}")
+    assert err < TOL_BF16
+
+
 def test_encoder_f32_batched_rows_layout(gpu):
     rng = np.random.default_rng(3)
     b, h, t, d = 2, 2, 700, 64
