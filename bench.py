@@ -339,6 +339,40 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
     torch.cuda.synchronize()
     us_build = e0.elapsed_time(e1) * 1e3 / reps
     build_bytes = layers * 2 * T_enc * row * (4 + 2)
+    # the prompt step (step 0 of a window): 228 tokens appended to a one-slot stack, causal
+    # self-attention at offset 0 and cross-attention over the window's frames, every layer
+    from ffai_amd.kv_cache import self_attention_step
+    P = 228
+    pstack = KVCache(1, H, cap, D, bf, dev, layers=layers)
+    pk = torch.randn(1, P, H * D, generator=gd, device=dev)
+    pv = torch.randn(1, P, H * D, generator=gd, device=dev)
+    pq = torch.randn(1, H, P, D, generator=gd, device=dev).to(bf)
+    po = torch.empty(1, H, P, D, device=dev, dtype=torch.float32)
+    pws = torch.empty(max(1, fa.workspace_bytes(pq, xs[0][2][None], xs[0][3][None], po,
+                                                k_transposed=True, scale=scale)),
+                      dtype=torch.uint8, device=dev)
+
+    def prompt_step():
+        for l in range(layers):
+            self_attention_step(pstack.layer(l), pq, pk, pv, 0, scale, out=po, workspace=pws)
+            fa.attention(pq, xs[l][2][None], xs[l][3][None], k_transposed=True, scale=scale,
+                         out=po, workspace=pws)
+
+    pstack.lens.zero_()
+    torch.cuda.synchronize()
+    pg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(pg):
+        prompt_step()
+    torch.cuda.synchronize()
+    preps = 20
+    e0.record()
+    for _ in range(preps):
+        pstack.lens.zero_()
+        pg.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_prompt = e0.elapsed_time(e1) * 1e3 / preps
+    prompt_flop = layers * 4.0 * D * H * (P * (P + 1) / 2 + P * T_enc)
     return {
         "state_us_per_step": us_state,
         "state_bytes_per_step": state_bytes,
@@ -347,6 +381,9 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
         "mean_self_len": mean_len,
         "cross_build_us_per_window": us_build,
         "cross_build_gbps": build_bytes / (us_build * 1e-6) / 1e9,
+        "prompt_step_us": us_prompt,
+        "prompt_step_tflops": prompt_flop / (us_prompt * 1e-6) / 1e12,
+        "prompt_tokens": P,
         "launches_per_step": layers + 1,
     }
 
@@ -440,7 +477,8 @@ def main():
         log("decode state: append + beam reorder, whisper-medium ...")
         st = decode_state_bench(torch, fa, 100, 10)
         log(f"decode state: {st['state_us_per_step']:.1f} us/step ({st['state_gbps']:.0f} GB/s), "
-            f"full step {st['full_step_us']:.1f} us, cross build {st['cross_build_us_per_window']:.1f} us")
+            f"full step {st['full_step_us']:.1f} us, cross build {st['cross_build_us_per_window']:.1f} us, "
+            f"prompt step {st['prompt_step_us']:.1f} us ({st['prompt_step_tflops']:.1f} TFLOP/s)")
         extras["decode_state_beam5"] = st
     if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")

@@ -81,21 +81,28 @@ struct AppendParams {
   int64_t ks, kh, kp;          // cache slot, head, position strides
   int32_t heads, head_dim, capacity, t_new;
   int32_t src_vec, dst_vec;    // 8-element vector accesses are aligned
+  int32_t units_per_block;     // 8-element units of one slot's rows per workgroup
+  int32_t advance;             // this launch also advances lens (one workgroup per slot)
 };
 
-// One workgroup per slot: every thread reads lens[slot] before the barrier, thread 0 advances it
-// after, so the position each row lands on is fixed for the whole call.
+// Workgroup (slot, blockIdx.y) moves units [y * units_per_block, ...) of the slot's t_new rows
+// to positions lens[slot] + t. With one workgroup per slot (`advance`) every thread reads
+// lens[slot] before the barrier and thread 0 advances it after, so the position each row lands
+// on is fixed for the whole call; with several, kv_advance_kernel advances lens afterwards (the
+// workgroups of one slot cannot order their reads of lens before its update).
 template <int SRC, int DST>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int s = blockIdx.x;
   const int len0 = p.lens[s];
   const int row_units = p.heads * p.head_dim / 8;
   const int units = p.t_new * row_units;
+  const int u_begin = blockIdx.y * p.units_per_block;
+  const int u_end = min(units, u_begin + p.units_per_block);
   const auto* sk = reinterpret_cast<const store_t<SRC>*>(p.src_k) + (int64_t)s * p.src_ss;
   const auto* sv = reinterpret_cast<const store_t<SRC>*>(p.src_v) + (int64_t)s * p.src_ss;
   auto* dk = reinterpret_cast<store_t<DST>*>(p.k) + (int64_t)s * p.ks;
   auto* dv = reinterpret_cast<store_t<DST>*>(p.v) + (int64_t)s * p.ks;
-  for (int u = threadIdx.x; u < units; u += 256) {
+  for (int u = u_begin + threadIdx.x; u < u_end; u += 256) {
     const int t = u / row_units;
     const int col = (u - t * row_units) * 8;  // h * head_dim + d
     const int h = col / p.head_dim, d = col - h * p.head_dim;
@@ -109,8 +116,16 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
     load8<SRC>(sv + so, p.src_vec, x);
     store8<DST>(dv + doff, p.dst_vec, x);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) p.lens[s] = min(p.capacity, len0 + p.t_new);
+  if (p.advance) {
+    __syncthreads();
+    if (threadIdx.x == 0) p.lens[s] = min(p.capacity, len0 + p.t_new);
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* lens, int slots, int capacity,
+                                                         int t_new) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  if (s < slots) lens[s] = min(capacity, lens[s] + t_new);
 }
 
 struct GatherParams {
@@ -265,8 +280,19 @@ hipError_t dispatch2(int src, int dst, A&&... a) {
 
 template <int S, int D>
 struct AppendLaunch {
-  static hipError_t run(const AppendParams& p, int slots, hipStream_t st) {
-    hipLaunchKernelGGL((kv_append_kernel<S, D>), dim3(slots), dim3(256), 0, st, p);
+  // A slot's rows go to ceil(units / kUnitsPerBlock) workgroups: one for a decode step's single
+  // row (lens advanced in the same launch), several for a prompt's hundreds (then a second,
+  // one-thread-per-slot launch advances lens).
+  static constexpr int kUnitsPerBlock = 4096;
+  static hipError_t run(AppendParams p, int slots, hipStream_t st) {
+    const int64_t units = (int64_t)p.t_new * p.heads * p.head_dim / 8;
+    const int64_t nblk = (units + kUnitsPerBlock - 1) / kUnitsPerBlock;
+    p.units_per_block = kUnitsPerBlock;
+    p.advance = nblk == 1;
+    hipLaunchKernelGGL((kv_append_kernel<S, D>), dim3(slots, (unsigned)nblk), dim3(256), 0, st, p);
+    if (nblk > 1)
+      hipLaunchKernelGGL(kv_advance_kernel, dim3((slots + 255) / 256), dim3(256), 0, st, p.lens,
+                         slots, p.capacity, p.t_new);
     return hipGetLastError();
   }
 };
@@ -322,6 +348,8 @@ int ffai_kv_append(const ffai_kv_cache* c, const void* new_k, const void* new_v,
   if (sdt < 0) return api_fail(FFAI_ERR_INVALID, "unknown source dtype");
   if (!new_k || !new_v) return api_fail(FFAI_ERR_INVALID, "null source pointer");
   if (t_new < 0) return api_fail(FFAI_ERR_INVALID, "t_new must be >= 0");
+  if ((int64_t)t_new * c->heads * c->head_dim / 8 >= (int64_t(1) << 31))
+    return api_fail(FFAI_ERR_INVALID, "t_new * heads * head_dim too large");
   if (src_row_stride < (int64_t)c->heads * c->head_dim || src_slot_stride < 0)
     return api_fail(FFAI_ERR_INVALID, "bad source strides");
   if ((uintptr_t)new_k % esize(sdt) || (uintptr_t)new_v % esize(sdt))

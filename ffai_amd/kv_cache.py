@@ -101,3 +101,28 @@ def cross_kv_build(k_proj: torch.Tensor, v_proj: torch.Tensor, heads: int,
         k.data_ptr(), v.data_ptr(), _DT[out_dtype],
         L.K_TRANSPOSED if k_transposed else L.K_ROWS, _stream_handle(k_proj)))
     return k, v
+
+
+def self_attention_step(cache: KVCache, q: torch.Tensor, k_new: torch.Tensor,
+                        v_new: torch.Tensor, offset: int, scale: float,
+                        out: Optional[torch.Tensor] = None,
+                        workspace: Optional[torch.Tensor] = None,
+                        out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Attention::forward_self (crates/ffai-mercury/src/asr/text_decoder.rs:652-679) on the
+    device: append this step's K/V projections to the cache in place (replacing Tensor::cat),
+    then attend q over every slot's keys. A multi-token step (a prompt, :663-676) is causal:
+    query i sits at absolute position offset + i and sees keys 0..offset + i (causal_mask,
+    :902-923); a single-token step needs no mask, as in the reference.
+
+    q: (slots, heads, q_len, head_dim); k_new, v_new: (slots, q_len, heads * head_dim);
+    `offset` is the absolute position of the first query token, which the caller knows (the
+    cache's lengths before the append), exactly as the reference's caller passes it.
+    The weights are softmax(scale * q k^T): scale = head_dim^-0.5 reproduces the reference's
+    q * s^2 (:840)."""
+    from . import flash_attn as fa
+
+    cache.append(k_new, v_new)
+    q_len = q.shape[2]
+    return fa.attention(q, cache.k, cache.v, scale=scale, kv_lens=cache.lens,
+                        causal=q_len > 1, q_offset=offset if q_len > 1 else 0, out=out,
+                        workspace=workspace, out_dtype=out_dtype)

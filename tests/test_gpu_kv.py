@@ -59,6 +59,31 @@ def test_append_matches_concatenation(gpu, src, dst):
         np.testing.assert_array_equal(v[s, :, :n], want_v)
 
 
+def test_long_append_spans_workgroups(gpu):
+    """A 200-row append (a prompt's size: 25600 8-element units per slot, several workgroups per
+    slot and a separate length update) into ragged slots, one of which runs past capacity."""
+    rng = np.random.default_rng(16)
+    slots, heads, d, cap, t_new = 3, 16, 64, 448, 200
+    start = np.array([0, 10, 300], np.int32)
+    cache = KVCache(slots, heads, cap, d, torch.bfloat16, gpu)
+    old_k = okv.round_to(randn(rng, cache.k.shape), "bf16")
+    cache.k.copy_(torch.from_numpy(old_k))
+    cache.lens.copy_(torch.from_numpy(start))
+    nk = randn(rng, (slots, t_new, heads * d))
+    nv = randn(rng, (slots, t_new, heads * d))
+    cache.append(_dev(nk, torch.float32, gpu), _dev(nv, torch.float32, gpu))
+    lens = cache.lens.cpu().numpy()
+    np.testing.assert_array_equal(lens, np.minimum(start + t_new, cap))
+    k, v = cache.k.float().cpu().numpy(), cache.v.float().cpu().numpy()
+    for s in range(slots):
+        n = int(lens[s] - start[s])
+        want_k = okv.round_to(okv.split_heads(nk[s:s + 1, :n], heads)[0], "bf16")
+        want_v = okv.round_to(okv.split_heads(nv[s:s + 1, :n], heads)[0], "bf16")
+        np.testing.assert_array_equal(k[s, :, start[s]:lens[s]], want_k)
+        np.testing.assert_array_equal(v[s, :, start[s]:lens[s]], want_v)
+        np.testing.assert_array_equal(k[s, :, :start[s]], old_k[s, :, :start[s]])  # untouched
+
+
 def test_gather_follows_parents(gpu):
     rng = np.random.default_rng(11)
     slots, heads, d, cap = 5, 16, 64, 448

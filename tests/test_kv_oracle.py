@@ -3,6 +3,8 @@ reference's operations fix (CPU only)."""
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 
@@ -56,3 +58,39 @@ def test_round_to_nearest_even():
     np.testing.assert_array_equal(kv.round_to(x, "bf16"), [1.0, 1 + 2 ** -6, 1 + 2 ** -7])
     # f16 keeps 11: 1 + 2^-11 ties -> 1
     np.testing.assert_array_equal(kv.round_to(np.array([1 + 2 ** -11], np.float32), "f16"), [1.0])
+
+
+def test_causal_mask_brute_force():
+    """Element by element: -inf exactly where key j > offset + i (text_decoder.rs:902-923)."""
+    for q_len, k_len, offset in [(1, 1, 0), (4, 4, 0), (3, 8, 5), (5, 7, 1)]:
+        m = kv.causal_mask(q_len, k_len, offset)
+        assert m.shape == (q_len, k_len) and m.dtype == np.float32
+        for i in range(q_len):
+            for j in range(k_len):
+                assert (m[i, j] == -np.inf) == (j > offset + i) and (m[i, j] in (0.0, -np.inf))
+    # a prompt at offset 0 sees a lower triangle; the steady-state single token sees everything
+    assert (np.isneginf(kv.causal_mask(4, 4, 0)) == np.triu(np.ones((4, 4), bool), 1)).all()
+    assert not np.isneginf(kv.causal_mask(1, 9, 8)).any()
+
+
+def test_three_op_attend_against_brute_force_loops():
+    """Tiny case by explicit Python loops: masked softmax over keys, then the weighted sum."""
+    rng = np.random.default_rng(3)
+    b, h, tq, tk, d = 1, 2, 3, 5, 4
+    q, k, v = (rng.standard_normal(s).astype(np.float32) for s in
+               ((b, h, tq, d), (b, h, tk, d), (b, h, tk, d)))
+    mask = kv.causal_mask(tq, tk, 2)
+    got = kv.three_op_attend(q, k, v, 0.5, mask)
+    for hh in range(h):
+        for i in range(tq):
+            s = [sum(0.5 * float(q[0, hh, i, t]) * float(k[0, hh, j, t]) for t in range(d))
+                 + float(mask[i, j]) for j in range(tk)]
+            mx = max(s)
+            w = [math.exp(x - mx) for x in s]
+            z = sum(w)
+            for t in range(d):
+                want = sum(w[j] / z * float(v[0, hh, j, t]) for j in range(tk))
+                assert abs(got[0, hh, i, t] - want) < 1e-5
+    # a fully visible row with all scores equal averages V
+    same = kv.three_op_attend(np.zeros((1, 1, 1, d), np.float32), k[:, :1], v[:, :1], 1.0)
+    np.testing.assert_allclose(same[0, 0, 0], v[0, 0].mean(axis=0), rtol=1e-6, atol=1e-6)
