@@ -10,13 +10,14 @@ Also reported: the beam-5 decode step at the whisper-medium shape (24 layers of 
 self-attention over ragged per-beam caches plus cross-attention over 1500 shared encoder frames,
 bf16 K/V, f32 output), the device-resident decode state of that step (K/V append in place and
 beam reorder, with and without the attention calls, and the per-window cross-attention cache
-build), the whisper-tiny f32 and whisper-small bf16 encoders, the
+build), the whole whisper-large-v3 encoder self-attention block (hipBLASLt projections around
+the fused kernel), the whisper-tiny f32 and whisper-small bf16 encoders, the
 Qwen2-VL-2B-shape causal prefill (12 query heads over 2 K/V heads, head_dim 128, S = 4096), and
 the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this host's cores on a
 bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras]
-                       [--layers L] [--legs decode,state,tiny,small,prefill | none | copy]
+                       [--layers L] [--legs decode,state,block,tiny,small,prefill | none | copy]
 """
 
 from __future__ import annotations
@@ -43,9 +44,9 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--legs", default="decode,state,tiny,small,prefill",
+    ap.add_argument("--legs", default="decode,state,block,tiny,small,prefill",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "state, tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
+                         "state, block, tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
                          "calibration used to scale HBM byte counters")
     return ap.parse_args()
 
@@ -389,6 +390,55 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
 
 
 # ------------------------------------------------------------------------------------------
+# Encoder self-attention block (whisper-large-v3: projections + attention + out-projection)
+# ------------------------------------------------------------------------------------------
+
+def encoder_block_bench(torch, fa, steps, warmup, layers=4, windows=16, T=1500, n=1280, H=20):
+    """The whole EncoderAttention::forward per layer through ffai_encoder_attn_fwd, one call per
+    1500-frame window as the reference runs it (text_decoder.rs:1069-1076): the q, v, k^T and
+    out projections on hipBLASLt (bf16, f32 accumulation, bias epilogues) around the fused
+    attention, which reads the projections by stride. `windows` windows per layer (the
+    large-v3 batch of 16), distinct weights and activations per layer. FLOP per window =
+    4 GEMMs x 2 T n^2 + the attention's 4 H T^2 hd."""
+    from ffai_amd.encoder import EncoderAttention
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(6)
+    bf = torch.bfloat16
+    blocks = []
+    for _ in range(layers):
+        w = [(torch.randn(n, n, generator=g, device=dev) / n ** 0.5).to(bf) for _ in range(4)]
+        bias = [(0.1 * torch.randn(n, generator=g, device=dev)).to(bf) for _ in range(3)]
+        ea = EncoderAttention.load(n, H, w[0], bias[0], w[1], w[2], bias[1], w[3], bias[2])
+        xs = [torch.randn(1, T, n, generator=g, device=dev).to(bf) for _ in range(windows)]
+        blocks.append((ea, xs, [torch.empty_like(x) for x in xs]))
+    ws = torch.empty(blocks[0][0].workspace_bytes(blocks[0][1][0]), dtype=torch.uint8, device=dev)
+
+    def step():
+        for ea, xs, outs in blocks:
+            for x, out in zip(xs, outs):
+                ea(x, out=out, workspace=ws)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_window = e0.elapsed_time(e1) / (steps * layers * windows)
+    gemm_flop = 4 * 2.0 * T * n * n
+    attn_flop = 4.0 * H * T * T * (n // H)
+    return {"ms_per_window": ms_window,
+            "tflops": (gemm_flop + attn_flop) / (ms_window * 1e-3) / 1e12,
+            "gemm_gflop_per_window": gemm_flop / 1e9, "attn_gflop_per_window": attn_flop / 1e9,
+            "layers": layers, "windows": windows}
+
+
+# ------------------------------------------------------------------------------------------
 # CPU baseline: the oracle (reference algorithm restated) on this host's cores
 # ------------------------------------------------------------------------------------------
 
@@ -480,6 +530,12 @@ def main():
             f"full step {st['full_step_us']:.1f} us, cross build {st['cross_build_us_per_window']:.1f} us, "
             f"prompt step {st['prompt_step_us']:.1f} us ({st['prompt_step_tflops']:.1f} TFLOP/s)")
         extras["decode_state_beam5"] = st
+    if "block" in legs:
+        log("encoder block: whisper-large-v3 projections + attention + out-projection ...")
+        blk = encoder_block_bench(torch, fa, max(args.steps // 4, 3), 1)
+        log(f"encoder block: {blk['ms_per_window']:.3f} ms per window-layer, "
+            f"{blk['tflops']:.1f} TFLOP/s")
+        extras["encoder_block_large_v3"] = blk
     if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")
         tiny = encoder_bench(torch, fa, max(args.steps * 5, 50), args.warmup, 4, B=1, H=6,

@@ -48,6 +48,15 @@ class KVCacheView(ctypes.Structure):
     ]
 
 
+class EncoderAttnDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("dtype", "batch", "seq", "n_state", "n_head", "reserved0")]
+
+
+class EncoderAttnWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("wq", "bq", "wk_scaled", "wv", "bv", "wo", "bo")]
+
+
 class TensorView(ctypes.Structure):
     _fields_ = [
         ("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("on_device", ctypes.c_int32),
@@ -111,10 +120,14 @@ def load():
     L.ffai_kv_append.argtypes = [cp, vp, vp, i32, i32, i64, i64, vp]
     L.ffai_kv_gather.argtypes = [cp, cp, vp, i32, i64, i64, vp]
     L.ffai_cross_kv_build.argtypes = [vp, vp, i32, i32, i32, i32, i64, vp, vp, i32, i32, vp]
+    ed, ew = ctypes.POINTER(EncoderAttnDesc), ctypes.POINTER(EncoderAttnWeights)
+    L.ffai_encoder_attn_workspace_bytes.argtypes = [ed, ctypes.POINTER(ctypes.c_size_t)]
+    L.ffai_encoder_attn_fwd.argtypes = [ed, vp, ew, vp, vp, ctypes.c_size_t, vp]
     for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
-                 "ffai_cross_kv_build"):
+                 "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",
+                 "ffai_encoder_attn_fwd"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

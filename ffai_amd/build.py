@@ -1,9 +1,9 @@
 """Build the gfx950 attention library in-tree: ffai_amd/libffai_attn.so.
 
 hipcc compiles the kernel instantiations (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip, decode.hip),
-the decode-state kernels and their C ABI (kv_cache.hip), the launch dispatch (attn_launch.hip)
-and the attention C ABI (attn_api.cpp) for gfx950 only, in parallel, then links them into one
-shared library. Packed-FP32 VALU instructions are disabled for all device code.
+the decode-state kernels and their C ABI (kv_cache.hip), the launch dispatch (attn_launch.hip),
+the attention C ABI (attn_api.cpp) and the encoder attention block around hipBLASLt
+(encoder_attn.cpp) for gfx950 only, in parallel, then links them into one shared library. Packed-FP32 VALU instructions are disabled for all device code.
 """
 
 from __future__ import annotations
@@ -20,7 +20,8 @@ LIB_PATH = os.path.join(HERE, "libffai_attn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = [os.path.join(CSRC, n) for n in
            ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "kv_cache.hip",
-            "attn_launch.hip", "attn_api.cpp")]
+            "attn_launch.hip", "attn_api.cpp", "encoder_attn.cpp")]
+LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 ARCH = "gfx950"
 
 
@@ -71,7 +72,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB_PATH + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + LIBS, verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

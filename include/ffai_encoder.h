@@ -1,0 +1,68 @@
+/*
+ * ffai_encoder.h -- C ABI of the audio encoder's self-attention block on MI355X (gfx950):
+ * projections, fused attention and out-projection in one stream-ordered call.
+ *
+ * Replaces EncoderAttention::forward (crates/ffai-mercury/src/asr/text_decoder.rs:1059-1139):
+ *   q  = x Wq^T + bq                      (self.inner.query, :1088)
+ *   kt = Wk_scaled x^T  -> (heads, hd, T)  (key_wt_scaled.matmul(x.t()), :1090-1094; no bias)
+ *   v  = x Wv^T + bv                      (self.inner.value, :1097)
+ *   merged = attend_merged(q, kt, v)      (:1121-1125; scale already folded into Wk)
+ *   out = merged Wo^T + bo                (self.inner.out, :1126)
+ * The reference splits q and v into heads with a copy each (:1103-1117) and loops over batch
+ * items (:1069-1076). Here the projections land in the layouts the kernel reads by stride (no
+ * copies) and the batch is one launch per GEMM: hipBLASLt GEMMs with bias epilogues (bf16/f16
+ * in and out, f32 accumulation) around ffai_attn_fwd.
+ *
+ * All calls are asynchronous on `stream` (a hipStream_t; NULL = null stream), allocate nothing,
+ * take device pointers and return FFAI_OK or a negative ffai_status (ffai_attn.h), with the
+ * reason in ffai_attn_last_error().
+ */
+#ifndef FFAI_ENCODER_H
+#define FFAI_ENCODER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ffai_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ffai_encoder_attn_desc {
+  int32_t dtype;   /* FFAI_BF16 or FFAI_F16: x, weights, biases and out */
+  int32_t batch;   /* windows */
+  int32_t seq;     /* frames per window (1500 for 30 s of audio) */
+  int32_t n_state; /* model width; head_dim = n_state / n_head must be 64 or 128 */
+  int32_t n_head;
+  int32_t reserved0;
+} ffai_encoder_attn_desc;
+
+/* Weights in the reference's layout: each Linear weight is (out, in) row-major, each bias
+ * (out). wk_scaled is the key weight multiplied by head_dim^-0.5 once, at load
+ * (EncoderAttention::load, text_decoder.rs:1039-1050); the key projection has no bias. */
+typedef struct ffai_encoder_attn_weights {
+  const void* wq;
+  const void* bq;
+  const void* wk_scaled;
+  const void* wv;
+  const void* bv;
+  const void* wo;
+  const void* bo;
+} ffai_encoder_attn_weights;
+
+/* Bytes of device workspace ffai_encoder_attn_fwd needs for `d`: q, kt, v and the merged
+ * attention output in the compute dtype, the attention's own workspace, and GEMM scratch. */
+int ffai_encoder_attn_workspace_bytes(const ffai_encoder_attn_desc* d, size_t* bytes);
+
+/* x: (batch, seq, n_state) row-major; out: the same shape. workspace: at least
+ * ffai_encoder_attn_workspace_bytes(d), 256-byte aligned; its contents need no initialisation. */
+int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
+                          const ffai_encoder_attn_weights* w, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFAI_ENCODER_H */

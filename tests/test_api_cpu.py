@@ -267,3 +267,23 @@ def test_cross_kv_build_rejects_bad_arguments(lib):
     assert rc(rs=1000) == L.FFAI_ERR_INVALID
     assert rc(layout=9) == L.FFAI_ERR_INVALID
     assert rc(odt=5) == L.FFAI_ERR_INVALID
+
+
+def test_encoder_attn_rejects_bad_arguments(lib):
+    def desc(dtype=L.BF16, batch=1, seq=1500, n_state=1280, n_head=20):
+        d = L.EncoderAttnDesc()
+        d.dtype, d.batch, d.seq, d.n_state, d.n_head = dtype, batch, seq, n_state, n_head
+        return d
+
+    n = ctypes.c_size_t(0)
+    assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(desc()), ctypes.byref(n)) == L.FFAI_OK
+    act = 1500 * 1280 * 2
+    assert n.value >= 4 * act  # q, k^T, v and the merged output at least
+    for bad in (desc(dtype=L.F32), desc(n_head=7), desc(n_state=640, n_head=20), desc(seq=0),
+                desc(batch=16)):  # more than one 1500-frame window of rows per call
+        assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(bad), ctypes.byref(n)) == \
+            L.FFAI_ERR_INVALID
+    w = L.EncoderAttnWeights()  # all null
+    assert lib.ffai_encoder_attn_fwd(ctypes.byref(desc()), FAKE, ctypes.byref(w), FAKE, FAKE,
+                                     1 << 40, None) == L.FFAI_ERR_INVALID
+    assert "null" in L.last_error()
