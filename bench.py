@@ -11,13 +11,14 @@ self-attention over ragged per-beam caches plus cross-attention over 1500 shared
 bf16 K/V, f32 output), the device-resident decode state of that step (K/V append in place and
 beam reorder, with and without the attention calls, and the per-window cross-attention cache
 build), the whole whisper-large-v3 encoder self-attention block (hipBLASLt projections around
-the fused kernel), the whisper-tiny f32 and whisper-small bf16 encoders, the
+the fused kernel), the decoder GEMVs of a beam-5 step (f16 projections, int8 vocabulary),
+the whisper-tiny f32 and whisper-small bf16 encoders, the
 Qwen2-VL-2B-shape causal prefill (12 query heads over 2 K/V heads, head_dim 128, S = 4096), and
 the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this host's cores on a
 bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras]
-                       [--layers L] [--legs decode,state,block,tiny,small,prefill | none | copy]
+                       [--layers L] [--legs decode,state,block,gemv,tiny,small,prefill | none | copy]
 """
 
 from __future__ import annotations
@@ -44,9 +45,9 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--legs", default="decode,state,block,tiny,small,prefill",
+    ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "state, block, tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
+                         "state, block, gemv, tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
                          "calibration used to scale HBM byte counters")
     return ap.parse_args()
 
@@ -439,6 +440,66 @@ def encoder_block_bench(torch, fa, steps, warmup, layers=4, windows=16, T=1500, 
 
 
 # ------------------------------------------------------------------------------------------
+# Decoder GEMVs of a beam-5 whisper-medium step (f16 projections + int8 vocabulary)
+# ------------------------------------------------------------------------------------------
+
+def gemv_bench(torch, steps, warmup, beams=5, n=1024, layers=24, vocab=51865):
+    """Every single-row projection of one decode step for all beams at once: per layer the
+    self-attention q, k, v, out and cross-attention q, out (n x n) and the MLP (4n x n, n x 4n)
+    as f16 GEMVs, then the block-scaled int8 vocabulary projection. Captured in a HIP graph.
+    Algorithmic bytes: every weight byte once (f16, int8 + block scales + corrections) plus the
+    activations read and outputs written."""
+    from ffai_amd.gemv import F16Gemv, Int8Vocab
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(8)
+    shapes = [(n, n)] * 6 + [(4 * n, n), (n, 4 * n)]
+    mats = [[F16Gemv(torch.randn(o, i, generator=g, device=dev) / i ** 0.5) for o, i in shapes]
+            for _ in range(layers)]
+    xs = {i: torch.randn(beams, i, generator=g, device=dev) for i in (n, 4 * n)}
+    ys = {o: torch.empty(beams, o, device=dev) for o in (n, 4 * n)}
+    iv = Int8Vocab(torch.randn(vocab, n, generator=g, device=dev) / n ** 0.5)
+    logits = torch.empty(beams, vocab, device=dev)
+    ws = torch.empty(iv.workspace_bytes(beams), dtype=torch.uint8, device=dev)
+
+    def step():
+        for layer in mats:
+            for m in layer:
+                m(xs[m.in_dim], out=ys[m.out_dim])
+        iv(xs[n], out=logits, workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    f16_bytes = layers * sum(o * i * 2 + beams * (i + o) * 4 for o, i in shapes)
+    vocab_bytes = vocab * n + vocab * (n // 32) * 4 + vocab * 4 + beams * (n + vocab) * 4
+    # the vocabulary projection alone
+    e0.record()
+    for _ in range(steps):
+        iv(xs[n], out=logits, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    us_vocab = e0.elapsed_time(e1) * 1e3 / steps
+    return {"us_per_step": us, "bytes_per_step": f16_bytes + vocab_bytes,
+            "gbps": (f16_bytes + vocab_bytes) / (us * 1e-6) / 1e9,
+            "vocab_us": us_vocab, "vocab_gbps": vocab_bytes / (us_vocab * 1e-6) / 1e9,
+            "launches_per_step": layers * len(shapes) + 2, "beams": beams}
+
+
+# ------------------------------------------------------------------------------------------
 # CPU baseline: the oracle (reference algorithm restated) on this host's cores
 # ------------------------------------------------------------------------------------------
 
@@ -536,6 +597,12 @@ def main():
         log(f"encoder block: {blk['ms_per_window']:.3f} ms per window-layer, "
             f"{blk['tflops']:.1f} TFLOP/s")
         extras["encoder_block_large_v3"] = blk
+    if "gemv" in legs:
+        log("decoder GEMVs: beam-5 whisper-medium step ...")
+        gv = gemv_bench(torch, 50, 5)
+        log(f"decoder GEMVs: {gv['us_per_step']:.1f} us/step ({gv['gbps']:.0f} GB/s); vocabulary "
+            f"projection {gv['vocab_us']:.1f} us ({gv['vocab_gbps']:.0f} GB/s)")
+        extras["decoder_gemv_beam5"] = gv
     if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")
         tiny = encoder_bench(torch, fa, max(args.steps * 5, 50), args.warmup, 4, B=1, H=6,

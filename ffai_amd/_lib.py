@@ -123,11 +123,17 @@ def load():
     ed, ew = ctypes.POINTER(EncoderAttnDesc), ctypes.POINTER(EncoderAttnWeights)
     L.ffai_encoder_attn_workspace_bytes.argtypes = [ed, ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_encoder_attn_fwd.argtypes = [ed, vp, ew, vp, vp, ctypes.c_size_t, vp]
+    L.ffai_gemv_f16.argtypes = [vp, i32, i32, vp, i32, i64, vp, i64, vp]
+    L.ffai_vocab_int8_quantize.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp]
+    L.ffai_vocab_int8_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_size_t)]
+    L.ffai_vocab_int8_logits.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, i64, vp,
+                                         ctypes.c_size_t, vp]
     for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
                  "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",
-                 "ffai_encoder_attn_fwd"):
+                 "ffai_encoder_attn_fwd", "ffai_gemv_f16", "ffai_vocab_int8_quantize",
+                 "ffai_vocab_int8_workspace_bytes", "ffai_vocab_int8_logits"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

@@ -20,7 +20,7 @@ LIB_PATH = os.path.join(HERE, "libffai_attn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = [os.path.join(CSRC, n) for n in
            ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "kv_cache.hip",
-            "attn_launch.hip", "attn_api.cpp", "encoder_attn.cpp")]
+            "gemv.hip", "attn_launch.hip", "attn_api.cpp", "encoder_attn.cpp")]
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 ARCH = "gfx950"
 

@@ -1,0 +1,64 @@
+/*
+ * ffai_gemv.h -- C ABI of the decoder's single-row projections on MI355X (gfx950): the f16
+ * weight GEMV and the block-scaled int8 vocabulary projection.
+ *
+ * Replaces crates/ffai-mercury/src/asr/f16_gemv.rs (F16Gemv: f16 weights, f32 activations,
+ * f32 arithmetic) and crates/ffai-mercury/src/asr/vocab_int8.rs (Int8Vocab: one scale per
+ * 32-weight block, 7-bit offset activations, a per-row correction folded at load), the two
+ * HBM-bound operations of a decode step outside attention (text_decoder.rs:925-1006). Each
+ * call takes every beam's row at once, so the weights stream from HBM once per step instead
+ * of once per beam.
+ *
+ * All calls are asynchronous on `stream` (a hipStream_t; NULL = null stream), allocate nothing,
+ * take device pointers and return FFAI_OK or a negative ffai_status (ffai_attn.h), with the
+ * reason in ffai_attn_last_error().
+ */
+#ifndef FFAI_GEMV_H
+#define FFAI_GEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ffai_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* y[r][o] = sum_i W[o][i] * x[r][i] for r < rows: W (out_dim, in_dim) f16 row-major (the
+ * layout QLinear stores, F16Gemv::new, f16_gemv.rs:88-115), x f32 rows (row stride
+ * x_row_stride), y f32 rows (row stride y_row_stride). in_dim a multiple of 8 (the reference's
+ * decline rule, :101-103), rows <= 16. Products in f32 (F16Gemv::forward / dot_f16,
+ * :117-196); the summation order differs from the reference's 16-lane AVX order, so results
+ * agree to f32 rounding, not bit for bit. */
+int ffai_gemv_f16(const void* w, int32_t out_dim, int32_t in_dim, const float* x, int32_t rows,
+                  int64_t x_row_stride, float* y, int64_t y_row_stride, void* stream);
+
+/* Int8Vocab::new (vocab_int8.rs:100-170): quantize the (vocab, d) embedding matrix (f32, f16
+ * or bf16, row-major) with one scale per `blk` weights: scale = amax / 127 (1 where the block
+ * is all zero), q = round-half-away(w / scale) clamped to [-127, 127]; corr[v] =
+ * 64 * sum_b scale_b * sum(q of block b), summed over blocks in order. Writes qw (vocab * d
+ * int8), bscale (vocab * d / blk f32) and corr (vocab f32). blk a multiple of 32 dividing d.
+ * Bit-identical to the reference's arithmetic (IEEE f32, no fused multiply-add). */
+int ffai_vocab_int8_quantize(const void* emb, int32_t emb_dtype, int32_t vocab, int32_t d,
+                             int32_t blk, int8_t* qw, float* bscale, float* corr, void* stream);
+
+/* Bytes of device workspace ffai_vocab_int8_logits needs (the quantized activations). */
+int ffai_vocab_int8_workspace_bytes(int32_t d, int32_t rows, size_t* bytes);
+
+/* Int8VocabOp::cpu_fwd (vocab_int8.rs:223-262) for `rows` activation rows (one per beam) at
+ * once: per row, sx = amax(x) / 63 (1 if x is all zero), x_u = round-half-away(x / sx)
+ * clamped to [-64, 63] plus 64; per vocab row v, acc = sum over blocks b, in order, of
+ * (dot(x_u, q) over the block as an exact integer) * bscale[v][b]; logit = (acc - corr[v]) * sx.
+ * x: rows x d f32 (row stride x_row_stride); logits: rows x vocab f32 (row stride
+ * logits_row_stride). Bit-identical to the reference's arithmetic. */
+int ffai_vocab_int8_logits(const int8_t* qw, const float* bscale, const float* corr,
+                           int32_t vocab, int32_t d, int32_t blk, const float* x, int32_t rows,
+                           int64_t x_row_stride, float* logits, int64_t logits_row_stride,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFAI_GEMV_H */

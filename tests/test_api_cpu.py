@@ -287,3 +287,18 @@ def test_encoder_attn_rejects_bad_arguments(lib):
     assert lib.ffai_encoder_attn_fwd(ctypes.byref(desc()), FAKE, ctypes.byref(w), FAKE, FAKE,
                                      1 << 40, None) == L.FFAI_ERR_INVALID
     assert "null" in L.last_error()
+
+
+def test_gemv_entry_points_reject_bad_arguments(lib):
+    assert lib.ffai_gemv_f16(FAKE, 1024, 1020, FAKE, 5, 1020, FAKE, 1024, None) == L.FFAI_ERR_INVALID
+    assert lib.ffai_gemv_f16(FAKE, 1024, 1024, FAKE, 17, 1024, FAKE, 1024, None) == L.FFAI_ERR_INVALID
+    assert lib.ffai_gemv_f16(None, 1024, 1024, FAKE, 5, 1024, FAKE, 1024, None) == L.FFAI_ERR_INVALID
+    # f16_gemv.rs:101-103 declines in_dim not a multiple of 8; vocab_int8.rs:131-133 needs a
+    # block a multiple of 32 that tiles d
+    assert lib.ffai_vocab_int8_quantize(FAKE, L.F32, 100, 384, 48, FAKE, FAKE, FAKE, None) == L.FFAI_ERR_INVALID
+    assert lib.ffai_vocab_int8_quantize(FAKE, L.F32, 100, 400, 32, FAKE, FAKE, FAKE, None) == L.FFAI_ERR_INVALID
+    n = ctypes.c_size_t(0)
+    assert lib.ffai_vocab_int8_workspace_bytes(1024, 5, ctypes.byref(n)) == L.FFAI_OK
+    assert n.value >= 5 * 1024 + 5 * 4
+    assert lib.ffai_vocab_int8_logits(FAKE, FAKE, FAKE, 51865, 1024, 32, FAKE, 5, 1024, FAKE,
+                                      51865, FAKE, 1, None) == L.FFAI_ERR_WORKSPACE
