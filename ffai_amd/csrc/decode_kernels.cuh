@@ -14,6 +14,8 @@
 //     all of a unit's partials in LDS with one round of loads and merges them. (An in-kernel
 //     last-arriver merge needs a device-scope release per workgroup, which on this GPU writes
 //     back the L2 and serialises: measured slower than the second launch.)
+//   * each wave's tile region is its own: whole tiles arrive by DMA (global -> LDS, no staging
+//     registers) into unpadded, XOR-swizzled rows, and a wave waits only for its own loads;
 //   * the tile loop is not unrolled: a cold workgroup fetches little code.
 // MFMA operands and fragment layouts are those of fwd_kernel's 16-bit path (attn_kernels.cuh).
 #pragma once
@@ -37,10 +39,12 @@ __device__ __forceinline__ void store_row_chunk(const DecodeParams& p, int b, in
 template <int MODE, int OUTT, int D, bool KT, int NWD>
 __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   static_assert(MODE == kBF16 || MODE == kF16, "decode kernel reads 16-bit Q, K and V");
-  // Per-wave LDS: one K tile ([key][d] or [d][key]) and one V tile ([key][d]), 16-bit.
-  constexpr int KROW = D + 8;
-  constexpr int KTROW = BN + 8;
-  constexpr int VROW = D + 8;
+  // Per-wave LDS: one K tile ([key][d] or [d][key]) and one V tile ([key][d]), 16-bit, rows
+  // unpadded with each row's 16-byte chunks XOR-permuted (swz_*, as in fwd_kernel) so that whole
+  // tiles arrive by DMA and the fragment reads still spread over the banks.
+  constexpr int KROW = D;
+  constexpr int KTROW = BN;
+  constexpr int VROW = D;
   constexpr int KBUF = KT ? D * KTROW : BN * KROW;
   constexpr int VBUF = BN * VROW;
   constexpr int WBUF = KBUF + VBUF;  // 16-bit elements per wave
@@ -106,6 +110,10 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
 
   uint16_t* kl = lds + wave * WBUF;
   uint16_t* vl = kl + KBUF;
+  // 16-byte chunk permutations of the tiles' rows (the same as fwd_kernel's)
+  auto swz_kt = [](int r, int c) { return c ^ (4 * ((r >> 1) & 1)); };
+  auto swz_v = [](int r, int c) { return D == 64 ? c ^ (4 * ((r >> 1) & 1)) : c ^ (4 * (r & 3)); };
+  auto swz_kr = [](int r, int c) { return D == 64 ? c ^ ((r >> 1) & 7) : c ^ (r & 15); };
   const int jt = lane & 15;
   const int tr_row = jt >> 2, tr_col = 4 * (jt & 3);
   const int half16 = 16 * ((lane >> 4) & 1);
@@ -115,6 +123,37 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   //      and zeroed past it. K^T rows: 4-key (8-byte) chunks, each loaded when all four keys are
   //      valid and zeroed otherwise; the one chunk per row that straddles the last valid key is
   //      then patched element by element in LDS. Every address stays inside the operand.
+  // The wave's own tile, whole and aligned: global -> LDS by DMA (16-byte chunks, lane L of
+  // block j fills slot L of the block; the chunk placed there is the one the swizzle assigns).
+  auto dma_tile = [&](int it) {
+    const int kb = it * BN;
+    const uint32_t kla = lds_addr(kl), vla = lds_addr(vl);
+#pragma unroll
+    for (int j = 0; j < KBUF / 512; ++j) {
+      const int L = j * 64 + lane;
+      const uint16_t* src;
+      if constexpr (KT) {
+        const int r = L / (BN / 8), pc = L % (BN / 8);
+        src = kp + (int64_t)r * p.k_st + kb + 8 * swz_kt(r, pc);
+      } else {
+        const int r = L / (D / 8), pc = L % (D / 8);
+        src = kp + (int64_t)(kb + r) * p.k_st + 8 * swz_kr(r, pc);
+      }
+      lds_dma16(src, (uint32_t)__builtin_amdgcn_readfirstlane((int)(kla + j * 1024)));
+    }
+#pragma unroll
+    for (int j = 0; j < VBUF / 512; ++j) {
+      const int L = j * 64 + lane;
+      const int r = L / (D / 8), pc = L % (D / 8);
+      const uint16_t* src = vp + (int64_t)(kb + r) * p.v_st + 8 * swz_v(r, pc);
+      lds_dma16(src, (uint32_t)__builtin_amdgcn_readfirstlane((int)(vla + j * 1024)));
+    }
+  };
+  // Tail tiles (past the last valid key) and misaligned K^T rows: through registers. Rows of K
+  // and V: 16-byte units, the key index clamped to the last valid key and zeroed past it. K^T
+  // rows: 4-key (8-byte) chunks, each loaded when all four keys are valid and zeroed otherwise;
+  // the one chunk per row that straddles the last valid key is then patched element by element
+  // in LDS. Every address stays inside the operand; stores go to the swizzled slots.
   auto stage_tile = [&](int it) {
     const int kb = it * BN;
     const int klast = kv_end - 1;
@@ -143,13 +182,13 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       const int u = lane + 64 * j;
       if constexpr (KT) {
         const int d = u / (BN / 8), kc = u % (BN / 8);
-        *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * kc]) = kreg[j];
+        *reinterpret_cast<u32x4*>(&kl[d * KTROW + 8 * swz_kt(d, kc)]) = kreg[j];
       } else {
         const int key = u / (D / 8), c = u % (D / 8);
-        *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * c]) = kreg[j];
+        *reinterpret_cast<u32x4*>(&kl[key * KROW + 8 * swz_kr(key, c)]) = kreg[j];
       }
       const int key = u / (D / 8), c = u % (D / 8);
-      *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * c]) = vreg[j];
+      *reinterpret_cast<u32x4*>(&vl[key * VROW + 8 * swz_v(key, c)]) = vreg[j];
     }
     if constexpr (KT) {
       const int k4s = klast & ~3;  // the straddling chunk, when the valid keys end inside one
@@ -160,8 +199,10 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
 #pragma unroll
           for (int x = 0; x < 3; ++x) e[x] = row[min(k4s + x, klast)];
 #pragma unroll
-          for (int x = 0; x < 3; ++x)
-            if (k4s + x <= klast) kl[d * KTROW + (k4s - kb) + x] = e[x];
+          for (int x = 0; x < 3; ++x) {
+            const int col = k4s - kb + x;
+            if (k4s + x <= klast) kl[d * KTROW + 8 * swz_kt(d, col >> 3) + (col & 7)] = e[x];
+          }
         }
       }
     }
@@ -172,10 +213,12 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     const int it = t_begin + wave + NWD * i;
     const bool has = it < t_end;  // wave-uniform
     const int kb = it * BN;
-    if (i > 0) __syncthreads();  // the previous tile's LDS reads are done
-    if (has) stage_tile(it);
-    __syncthreads();
     if (!has) continue;
+    // the tile region is this wave's own: reuse needs only its own earlier LDS reads done
+    if (i > 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    if (kb + BN <= kv_end) dma_tile(it);
+    else stage_tile(it);
+    vm_wait_all();
 
     // ---- S^T for the tile's two 32-key subtiles: sacc[st][r] <-> key kb + 32st + 8(r/4) +
     //      4g + r%4 of row n32
@@ -188,11 +231,14 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       for (int s = 0; s < D / 16; ++s) {
         u32x4 a;
         if constexpr (KT) {
-          const uint16_t* base = &kl[(16 * s + 8 * g + tr_row) * KTROW + 32 * st + half16 + tr_col];
+          // rows r and r + 4 share the chunk permutation (it depends on bit 1 of the row)
+          const int r = 16 * s + 8 * g + tr_row, col = 32 * st + half16 + tr_col;
+          const uint16_t* base = &kl[r * KTROW + 8 * swz_kt(r, col >> 3) + (col & 7)];
           const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
           a = u32x4{lo.x, lo.y, hi.x, hi.y};
         } else {
-          a = *reinterpret_cast<const u32x4*>(&kl[(32 * st + n32) * KROW + 16 * s + 8 * g]);
+          const int r = 32 * st + n32;
+          a = *reinterpret_cast<const u32x4*>(&kl[r * KROW + 8 * swz_kr(r, 2 * s + g)]);
         }
         sacc[st] = mfma16<MODE>(a, qf[s], sacc[st]);
       }
@@ -242,7 +288,9 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
-        const uint16_t* base = &vl[(16 * t + 4 * g + tr_row) * VROW + 32 * dt + half16 + tr_col];
+        // rows r and r + 8 share the chunk permutation
+        const int r = 16 * t + 4 * g + tr_row, col = 32 * dt + half16 + tr_col;
+        const uint16_t* base = &vl[r * VROW + 8 * swz_v(r, col >> 3) + (col & 7)];
         const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
         oacc[dt] = mfma16<MODE>(u32x4{a0.x, a0.y, a1.x, a1.y}, pf[t], oacc[dt]);
       }

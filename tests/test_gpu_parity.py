@@ -156,9 +156,11 @@ def _views_with_high_low_word(gpu, arrays, dtype):
     31 set (the DMA path builds its 64-bit scalar base from two 32-bit halves)."""
     esz = torch.tensor([], dtype=dtype).element_size()
     sizes = [((a.size * esz + 255) // 256) * 256 for a in arrays]
-    buf = torch.empty(2 ** 31 + sum(sizes) + 4096, dtype=torch.uint8, device=gpu)
+    # start exactly at 2^31 (mod 2^32): the whole region then keeps bit 31 of the low word
+    buf = torch.empty(2 ** 32 + sum(sizes) + 4096, dtype=torch.uint8, device=gpu)
     lo = buf.data_ptr() & 0xFFFFFFFF
-    off = 0 if lo >= 2 ** 31 else ((2 ** 31 - lo + 255) // 256) * 256
+    off = (2 ** 31 - lo) % (2 ** 32)
+    assert off % 256 == 0  # allocations are at least 256-byte aligned
     out = []
     for a, n in zip(arrays, sizes):
         t = buf[off:off + a.size * esz].view(dtype).view(a.shape)
