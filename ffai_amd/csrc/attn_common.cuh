@@ -25,6 +25,12 @@ constexpr float kRescaleSlack = 8.0f;
 // 16-bit encoder kernel: a lane's sum of 16 weights above this (2^64) sends the subtile to the
 // exact-max path, so no weight exceeds it.
 constexpr float kWeightSumBound = 18446744073709551616.0f;
+// 16-bit encoder kernel: when every row max of a wave's first 32 keys lies in this window
+// (scaled log2 units), the wave takes 0 as every row's reference max, so a weight is exp2 of the
+// score itself: the largest weight of a row is then at least 2^-64, and a subtile's lane sum
+// starts far below kWeightSumBound.
+constexpr float kFastMaxLo = -64.0f;
+constexpr float kFastMaxHi = 32.0f;
 
 template <int DT>
 using store_t = std::conditional_t<DT == kF32, float, uint16_t>;

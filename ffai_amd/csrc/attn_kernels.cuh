@@ -19,10 +19,12 @@
 //     transposing LDS reads where an operand needs the other orientation. One barrier per tile.
 //   * Online softmax in base 2 with v_exp_f32. f32 kernel: the running max only moves when a
 //     tile's max exceeds it by more than 2^8 in probability. 16-bit kernels: no max is taken on
-//     the common path at all. Each row's reference max is the max of its first 32 keys, and
-//     weights are computed against it directly. A subtile whose weights would exceed 2^64 (or
-//     overflow) is redone against its exact max, with the accumulator rescaled; that is rare
-//     for real scores, and it keeps every weight and sum finite in f32.
+//     the common path at all. Q carries scale*log2(e), so scores come out of the first product
+//     in the exponent's units. When every row max of a wave's first 32 keys is moderate, the
+//     reference max is 0 and a weight is exp2 of the accumulator itself; otherwise it is that
+//     first max. A subtile whose weights would exceed 2^64 (or overflow) is redone against its
+//     exact max, with the accumulator rescaled; that is rare for real scores, and it keeps every
+//     weight and sum finite in f32.
 //   * Workgroup ids are remapped so that all query blocks of one (batch, kv-head) run on the
 //     same XCD (the hardware deals workgroup i to XCD i % 8) and share that XCD's L2.
 //   * Few-query shapes (decode) split the keys over workgroups; partial (O, m, l) go to the
@@ -492,6 +494,42 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // Probabilities are packed to 16 bits as they are produced; row sums use v_dot2 on the
     // packed pairs, i.e. they sum exactly the weights the second product consumes.
     // ---------------------------------------------------------------------------------------
+    // Fold scale*log2(e) into Q once (an f32 product rounded to the 16-bit type, the same
+    // rounding the inputs already carry), so that scores leave the first product in scaled log2
+    // units. If a scaled element would not be finite in the 16-bit type, the wave keeps Q as
+    // given and every score is multiplied instead (qmul).
+    float qmul = 1.f;
+    {
+      constexpr uint32_t kInfBits = MODE == kBF16 ? 0x7f80u : 0x7c00u;
+      u32x4 qs[QW][D / 16];
+      bool over = false;
+#pragma unroll
+      for (int c = 0; c < QW; ++c)
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) {
+          uint32_t w4[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t w = qf[c][s][k];
+            const uint32_t y =
+                pack2<MODE>(to_f32<MODE>(w & 0xffffu) * sl2, to_f32<MODE>(w >> 16) * sl2);
+            over = over || (y & 0x7fffu) >= kInfBits || ((y >> 16) & 0x7fffu) >= kInfBits;
+            w4[k] = y;
+          }
+          qs[c][s] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+        }
+      if (__builtin_amdgcn_ballot_w64(over) == 0) {
+#pragma unroll
+        for (int c = 0; c < QW; ++c)
+#pragma unroll
+          for (int s = 0; s < D / 16; ++s) qf[c][s] = qs[c][s];
+      } else {
+        qmul = sl2;
+      }
+    }
+    bool fast = false;  // m_s is 0 for every row of the wave and qmul is 1
+    constexpr std::integral_constant<bool, true> kFastTag{};
+    constexpr std::integral_constant<bool, false> kSlowTag{};
     constexpr int NQK = (D / 16) * QW;        // MFMAs per subtile in S^T
     constexpr int NPV = 2 * (D / 32) * QW;    // MFMAs per subtile in O^T
     u32x4 pf[QW][4];   // packed P: pf[c][t] = keys 16t..16t+15 of the tile, B-operand order
@@ -538,8 +576,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         uint32_t w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float e0 = fast_exp2(__builtin_fmaf(sv[8 * h2 + 2 * k], sl2, -mc));
-          const float e1 = fast_exp2(__builtin_fmaf(sv[8 * h2 + 2 * k + 1], sl2, -mc));
+          const float e0 = fast_exp2(__builtin_fmaf(sv[8 * h2 + 2 * k], qmul, -mc));
+          const float e1 = fast_exp2(__builtin_fmaf(sv[8 * h2 + 2 * k + 1], qmul, -mc));
           const uint32_t pk = pack2<MODE>(e0, e1);
           w[k] = pk;
           if constexpr (MODE == kBF16) {
@@ -554,18 +592,25 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       }
       return rs;
     };
-    // Fast path, inside the phase: weights against the current reference max m_s, with no max
-    // taken. m_s starts as the row max of the first subtile (set before the loop) and never
-    // exceeds the true running max, so the largest weight of a row is >= 1 and nothing that
-    // matters underflows; it is raised only in `settle`, when a subtile's weights leave the
-    // range below. Work unit: pair k (scores 2k, 2k+1) of column block c of subtile st.
+    // Common path, inside the phase: weights against the current reference max m_s, with no max
+    // taken. m_s starts either at 0 (FAST: every row max of the wave's first subtile lies in
+    // [kFastMaxLo, kFastMaxHi] and Q carries the scale, so a weight is exp2 of the accumulator
+    // itself) or at the row max of the first subtile; it is raised only in `settle`, when a
+    // subtile's weights leave the range below, and the wave then leaves FAST for good. Either
+    // way the largest weight of a row is at least 2^kFastMaxLo, so nothing that matters
+    // underflows. Work unit: pair k (scores 2k, 2k+1) of column block c of subtile st.
     constexpr int NPAIR = QW * 8;  // pairs per subtile
     uint32_t pw[QW][8];            // packed pairs of the subtile being exponentiated
-    auto exp_pair = [&](int st, int pidx) {
+    auto exp_pair = [&](int st, int pidx, auto fast_tag) {
+      constexpr bool FAST = decltype(fast_tag)::value;
       const int c = pidx >> 3, k = pidx & 7;
-      const float mc = m_s[c];
-      const float e0 = fast_exp2(__builtin_fmaf(sacc[c][st][2 * k], sl2, -mc));
-      const float e1 = fast_exp2(__builtin_fmaf(sacc[c][st][2 * k + 1], sl2, -mc));
+      float x0 = sacc[c][st][2 * k], x1 = sacc[c][st][2 * k + 1];
+      if constexpr (!FAST) {
+        x0 = __builtin_fmaf(x0, qmul, -m_s[c]);
+        x1 = __builtin_fmaf(x1, qmul, -m_s[c]);
+      }
+      const float e0 = fast_exp2(x0);
+      const float e1 = fast_exp2(x1);
       const uint32_t pk = pack2<MODE>(e0, e1);
       pw[c][k] = pk;
       if constexpr (MODE == kBF16) {
@@ -604,13 +649,17 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
           float mx = kNegInf;
 #pragma unroll
           for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sv[r], sv[r + 1]));
-          const float mx_s = partner_max(mx) * sl2;
+          const float mx_s = partner_max(mx) * qmul;
           const float m_old = m_s[c];
           const float m_new = fmaxf(m_old, mx_s);
           corr_s[c] = (m_new == m_old) ? 1.f : fast_exp2(m_old - m_new);
           m_s[c] = m_new;
           rs_s[c] = exps_c(sv, c, st, (m_new == kNegInf) ? 0.f : m_new);
         }
+        bool moved = false;
+#pragma unroll
+        for (int c = 0; c < QW; ++c) moved = moved || m_s[c] != 0.f;
+        fast = fast && __builtin_amdgcn_ballot_w64(moved) == 0;
       }
 #pragma unroll
       for (int c = 0; c < QW; ++c) l_run[c] = __builtin_fmaf(l_run[c], corr_s[c], rs_s[c]);
@@ -652,7 +701,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // other subtile, fenced so that the compiler keeps that order: one wave then keeps the
     // matrix pipe and the VALU busy together instead of issuing its MFMAs back to back.
     //   B: S^T(subtile 1) || exps(subtile 0);   C: O^T += V^T P^T(subtile 0) || exps(subtile 1)
-    auto phase_b = [&](const LT* kl) {
+    auto phase_b = [&](const LT* kl, auto fast_tag) {
       u32x4 a[D / 16];
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) a[s] = kfrag(kl, 1, s);
@@ -662,7 +711,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       for (int i = 0; i < NQK; ++i) {
         const int s = i / QW, c = i % QW;
 #pragma unroll
-        for (int j = i * NPAIR / NQK; j < (i + 1) * NPAIR / NQK; ++j) exp_pair(0, j);
+        for (int j = i * NPAIR / NQK; j < (i + 1) * NPAIR / NQK; ++j) exp_pair(0, j, fast_tag);
         sacc[c][1] = mfma16<MODE>(a[s], qf[c][s], sacc[c][1]);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -677,7 +726,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
       return u32x4{a0.x, a0.y, a1.x, a1.y};
     };
-    auto phase_c = [&](const LT* vl) {
+    auto phase_c = [&](const LT* vl, auto fast_tag) {
       u32x4 a[2][D / 32];
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
@@ -689,7 +738,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       for (int i = 0; i < NPV; ++i) {
         const int h2 = i / (QW * (D / 32)), dt = (i / QW) % (D / 32), c = i % QW;
 #pragma unroll
-        for (int j = i * NPAIR / NPV; j < (i + 1) * NPAIR / NPV; ++j) exp_pair(1, j);
+        for (int j = i * NPAIR / NPV; j < (i + 1) * NPAIR / NPV; ++j) exp_pair(1, j, fast_tag);
         oacc[c][dt] = mfma16<MODE>(a[h2][dt], pf[c][h2], oacc[c][dt]);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -714,13 +763,21 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       zero_sub(0);
       qk(sacc, k_lds, 0);
       if (need_mask_of(t_begin)) mask_subtile(sacc, t_begin * BN, 0);
-      // the reference max: this subtile's row max (-inf if all of it is masked)
+      // the reference max: this subtile's row max (-inf if all of it is masked), or 0 for the
+      // whole wave when every such max is in the FAST window
+      bool wide = false;
 #pragma unroll
       for (int c = 0; c < QW; ++c) {
         float mx = kNegInf;
 #pragma unroll
         for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[c][0][r], sacc[c][0][r + 1]));
-        m_s[c] = partner_max(mx) * sl2;
+        m_s[c] = partner_max(mx) * qmul;
+        wide = wide || !(m_s[c] >= kFastMaxLo && m_s[c] <= kFastMaxHi);
+      }
+      fast = qmul == 1.f && __builtin_amdgcn_ballot_w64(wide) == 0;
+      if (fast) {
+#pragma unroll
+        for (int c = 0; c < QW; ++c) m_s[c] = 0.f;
       }
     }
     for (int it = t_begin; it < t_end; ++it) {
@@ -732,14 +789,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       zero_sub(1);
       // B
       __builtin_amdgcn_sched_barrier(0);
-      phase_b(kl);
+      if (fast) phase_b(kl, kFastTag);
+      else phase_b(kl, kSlowTag);
       __builtin_amdgcn_sched_barrier(0);
       settle(0);
       rescale();
       if (need_mask) mask_subtile(sacc, kb, 1);
       // C
       __builtin_amdgcn_sched_barrier(0);
-      phase_c(vl);
+      if (fast) phase_c(vl, kFastTag);
+      else phase_c(vl, kSlowTag);
       __builtin_amdgcn_sched_barrier(0);
       settle(1);
       rescale();

@@ -151,6 +151,57 @@ def test_scores_far_above_the_first_subtile(gpu, dtype, k_transposed):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_first_subtile_outside_the_fast_window(gpu, dtype, sign):
+    """A wave takes 0 as its reference max only when every row max of its first 32 keys lies
+    in [-64, 32] log2 units. Here every score sits near +-87 log2 units, so the wave keeps the
+    first subtile's max instead (well above: weights would overflow; well below: they would
+    underflow to 0 and the rows would come out empty)."""
+    rng = np.random.default_rng(31)
+    b, h, t, d = 1, 2, 700, 64
+    rnd = round_bf16 if dtype == torch.bfloat16 else round_f16
+    u = np.zeros(d, np.float32)
+    u[5] = 1.0
+    q = rnd(8.0 * u + 0.05 * randn(rng, (b, h, t, d)))
+    k = rnd(np.float32(sign * 60.0) * u + randn(rng, (b, h, t, d)))
+    v = rnd(randn(rng, (b, h, t, d)))
+    scale = 0.125
+    out = fa.attention(_dev(q, dtype, gpu), _dev(k, dtype, gpu), _dev(v, dtype, gpu),
+                       scale=scale, out_dtype=torch.float32)
+    got = _host(out)
+    assert np.isfinite(got).all()
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=scale)
+    err = max_abs(got, want)
+    print(f"outside the fast window {dtype} sign={sign}: {err:.3e}")
+    assert err < TOL_BF16
+
+
+@pytest.mark.parametrize("k_transposed", [True, False])
+def test_f16_query_beyond_the_folding_range(gpu, k_transposed):
+    """The 16-bit kernel folds scale * log2(e) into Q. With scale 1, f16 query elements above
+    65504 / log2(e) ~ 45400 would overflow once folded, so such a wave keeps Q as given and
+    scales every score instead."""
+    rng = np.random.default_rng(32)
+    b, h, t, d = 1, 2, 400, 64
+    u = np.zeros(d, np.float32)
+    u[7] = 1.0
+    q = round_f16(50000.0 * u + randn(rng, (b, h, t, d)))
+    k = round_f16(np.float32(2e-4) * randn(rng, (b, h, t, d)))  # scores ~ N(0, 10)
+    v = round_f16(randn(rng, (b, h, t, d)))
+    assert np.abs(q).max() * 1.4426950408889634 > 65504.0
+    kk = np.ascontiguousarray(np.swapaxes(k, 2, 3)) if k_transposed else k
+    out = fa.attention(_dev(q, torch.float16, gpu), _dev(kk, torch.float16, gpu),
+                       _dev(v, torch.float16, gpu), k_transposed=k_transposed, scale=1.0,
+                       out_dtype=torch.float32)
+    got = _host(out)
+    assert np.isfinite(got).all()
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=1.0)
+    err = max_abs(got, want)
+    print(f"f16 q beyond the folding range kt={k_transposed}: {err:.3e}")
+    assert err < TOL_BF16
+
+
 def _views_with_high_low_word(gpu, arrays, dtype):
     """Device copies of `arrays` placed in one buffer at an address whose low 32 bits have bit
     31 set (the DMA path builds its 64-bit scalar base from two 32-bit halves)."""
