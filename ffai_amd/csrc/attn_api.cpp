@@ -191,7 +191,13 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok) {
   if (d->q_len > 32) p.variant = ffai::kWave4;
   if (!f32 && d->head_dim == 64 && d->q_len >= 256) p.variant = ffai::kWave4x2;
   if (p.variant == ffai::kWave4x2 && work_of(p.variant) < 256) p.variant = ffai::kWave4;
-  if (p.variant == ffai::kWave4 && work_of(p.variant) < 256) p.variant = ffai::kWave1;
+  // A one-wave workgroup holds a whole tile ring (48 KB of LDS in 16-bit, 68 KB in f32) for
+  // one wave, so at most three (two) of them run per CU. Short grids of 16-bit rows fewer than
+  // the encoder's (a prompt step: 228 rows) still run best on it; long runs and f32 keep four
+  // waves and split the keys instead (measured: whisper-large-v3 window, 20 heads x 1500 rows,
+  // bf16: 42.5 against 69.7 us; whisper-tiny f32: 66 against 154 us).
+  if (p.variant == ffai::kWave4 && work_of(p.variant) < 256 && !f32 && d->q_len < 256)
+    p.variant = ffai::kWave1;
   // FFAI_ATTN_VARIANT (0, 1, 2) forces a launch shape where it is instantiated: a tuning knob.
   static const int forced = [] {
     const char* e = std::getenv("FFAI_ATTN_VARIANT");

@@ -494,12 +494,14 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // Probabilities are packed to 16 bits as they are produced; row sums use v_dot2 on the
     // packed pairs, i.e. they sum exactly the weights the second product consumes.
     // ---------------------------------------------------------------------------------------
-    // Fold scale*log2(e) into Q once (an f32 product rounded to the 16-bit type, the same
-    // rounding the inputs already carry), so that scores leave the first product in scaled log2
-    // units. If a scaled element would not be finite in the 16-bit type, the wave keeps Q as
-    // given and every score is multiplied instead (qmul).
+    // head_dim 64: fold scale*log2(e) into Q once (an f32 product rounded to the 16-bit type,
+    // the same rounding the inputs already carry), so that scores leave the first product in
+    // scaled log2 units. If a scaled element would not be finite in the 16-bit type, the wave
+    // keeps Q as given and every score is multiplied instead (qmul).
     float qmul = 1.f;
-    {
+    if constexpr (D != 64) {
+      qmul = sl2;  // head_dim 128 keeps Q as given (the fold measured slower there)
+    } else {
       constexpr uint32_t kInfBits = MODE == kBF16 ? 0x7f80u : 0x7c00u;
       u32x4 qs[QW][D / 16];
       bool over = false;
@@ -774,7 +776,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         m_s[c] = partner_max(mx) * qmul;
         wide = wide || !(m_s[c] >= kFastMaxLo && m_s[c] <= kFastMaxHi);
       }
-      fast = qmul == 1.f && __builtin_amdgcn_ballot_w64(wide) == 0;
+      fast = D == 64 && qmul == 1.f && __builtin_amdgcn_ballot_w64(wide) == 0;
       if (fast) {
 #pragma unroll
         for (int c = 0; c < QW; ++c) m_s[c] = 0.f;
@@ -789,7 +791,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       zero_sub(1);
       // B
       __builtin_amdgcn_sched_barrier(0);
-      if (fast) phase_b(kl, kFastTag);
+      if (D == 64 && fast) phase_b(kl, kFastTag);
       else phase_b(kl, kSlowTag);
       __builtin_amdgcn_sched_barrier(0);
       settle(0);
@@ -797,7 +799,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       if (need_mask) mask_subtile(sacc, kb, 1);
       // C
       __builtin_amdgcn_sched_barrier(0);
-      if (fast) phase_c(vl, kFastTag);
+      if (D == 64 && fast) phase_c(vl, kFastTag);
       else phase_c(vl, kSlowTag);
       __builtin_amdgcn_sched_barrier(0);
       settle(1);
