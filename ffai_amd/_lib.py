@@ -54,7 +54,8 @@ class EncoderAttnDesc(ctypes.Structure):
 
 
 class EncoderAttnWeights(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in ("wq", "bq", "wk_scaled", "wv", "bv", "wo", "bo")]
+    _fields_ = [(n, ctypes.c_void_p)
+                for n in ("wq", "bq", "wk_scaled", "wv", "bv", "wo", "bo", "wqkv", "bqkv")]
 
 
 class TensorView(ctypes.Structure):

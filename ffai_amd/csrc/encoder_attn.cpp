@@ -10,6 +10,9 @@
 //                          (S, hd B S, B S, 1) -- one plain GEMM, no batched GEMM
 //   merged (B, S, N)     attention output, the kernel writing the merged layout directly
 //   attention workspace, then hipBLASLt scratch
+// With packed weights (wqkv, bqkv) the first three regions hold instead
+//   qkv    (B, S, 3N)    = x Wqkv^T + bqkv in one GEMM: q, k and v of one frame side by side,
+//                          read by the kernel with strides (S 3N, hd, 3N, 1) and K as rows
 // All GEMMs are column-major in hipBLASLt's terms: a row-major (rows, cols) matrix is a
 // column-major (cols, rows) one, so Y = X W^T (row-major, X (M, K), W (N, K)) is computed as
 // Y^T = W X^T with A = W (op T), B = X (op N), and the bias runs along Y^T's rows (features).
@@ -19,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <array>
 #include <cstring>
 #include <map>
@@ -168,29 +172,35 @@ int check(const ffai_encoder_attn_desc* d) {
   return FFAI_OK;
 }
 
-void attn_desc(const ffai_encoder_attn_desc* d, ffai_attn_desc* a) {
+// `packed`: q, k and v side by side in one (B, S, 3N) buffer, K read as rows.
+void attn_desc(const ffai_encoder_attn_desc* d, bool packed, ffai_attn_desc* a) {
   const int hd = d->n_state / d->n_head;
   const int64_t S = d->seq, N = d->n_state;
   ffai_attn_desc_init(a, d->dtype, d->dtype, d->dtype, d->batch, d->n_head, d->n_head, d->seq,
-                      d->seq, hd, FFAI_K_TRANSPOSED);
+                      d->seq, hd, packed ? FFAI_K_ROWS : FFAI_K_TRANSPOSED);
   a->scale = 1.0f;  // head_dim^-0.5 is folded into wk_scaled
-  const int64_t qs[4] = {S * N, hd, N, 1};          // q, v and the merged output: (B, S, N)
+  const int64_t os[4] = {S * N, hd, N, 1};          // the merged output (and unpacked q, v): (B, S, N)
+  const int64_t ps[4] = {S * 3 * N, hd, 3 * N, 1};  // packed q, k, v: (B, S, 3N)
   const int64_t BS = (int64_t)d->batch * S;
   const int64_t ks[4] = {S, (int64_t)hd * BS, BS, 1};   // kt: (N, B S) seen as (B, H, hd, S)
-  std::memcpy(a->q_strides, qs, sizeof(qs));
-  std::memcpy(a->v_strides, qs, sizeof(qs));
-  std::memcpy(a->o_strides, qs, sizeof(qs));
-  std::memcpy(a->k_strides, ks, sizeof(ks));
+  std::memcpy(a->q_strides, packed ? ps : os, sizeof(os));
+  std::memcpy(a->v_strides, packed ? ps : os, sizeof(os));
+  std::memcpy(a->k_strides, packed ? ps : ks, sizeof(os));
+  std::memcpy(a->o_strides, os, sizeof(os));
 }
 
 int sizes_of(const ffai_encoder_attn_desc* d, Sizes* z) {
   const size_t el = 2, act = (size_t)d->batch * d->seq * d->n_state * el;
   z->q = z->kt = z->v = z->merged = align256(act);
-  ffai_attn_desc a;
-  attn_desc(d, &a);
   size_t aw = 0;
-  const int rc = ffai_attn_workspace_bytes(&a, &aw);
-  if (rc != FFAI_OK) return rc;
+  for (const bool packed : {false, true}) {
+    ffai_attn_desc a;
+    attn_desc(d, packed, &a);
+    size_t b = 0;
+    const int rc = ffai_attn_workspace_bytes(&a, &b);
+    if (rc != FFAI_OK) return rc;
+    aw = std::max(aw, b);
+  }
   z->attn = align256(aw);
   z->gemm = kGemmScratch;
   z->total = z->q + z->kt + z->v + z->merged + z->attn + z->gemm;
@@ -219,8 +229,10 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   api_clear_error();
   int rc = check(d);
   if (rc != FFAI_OK) return rc;
-  if (!x || !out || !w || !w->wq || !w->bq || !w->wk_scaled || !w->wv || !w->bv || !w->wo || !w->bo)
-    return api_fail(FFAI_ERR_INVALID, "null pointer");
+  if (!x || !out || !w || !w->wo || !w->bo) return api_fail(FFAI_ERR_INVALID, "null pointer");
+  const bool packed = w->wqkv && w->bqkv;
+  if (!packed && (!w->wq || !w->bq || !w->wk_scaled || !w->wv || !w->bv))
+    return api_fail(FFAI_ERR_INVALID, "null pointer (give wq, bq, wk_scaled, wv, bv or wqkv, bqkv)");
   Sizes z;
   if ((rc = sizes_of(d, &z)) != FFAI_OK) return rc;
   if (!workspace || workspace_bytes < z.total)
@@ -247,6 +259,23 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   g.m = N; g.n = BS; g.k = N;
   g.lda = N; g.ldb = N; g.ldd = N;
   g.b = x;
+  ffai_attn_desc a;
+  attn_desc(d, packed, &a);
+  if (packed) {
+    // qkv: (B S, 3N) = x Wqkv^T + bqkv  ->  D^T (3N x BS) = Wqkv (op T) * x^T; the regions of
+    // q, kt and v are contiguous and hold it
+    Gemm gp = g;
+    gp.m = 3 * N; gp.ldd = 3 * N;
+    gp.a = w->wqkv; gp.d = q; gp.bias = w->bqkv;
+    if ((rc = run_gemm(h, gp, dt, scratch, z.gemm, st)) != FFAI_OK) return rc;
+    const size_t es = 2;
+    const char* qkv = static_cast<const char*>(q);
+    if ((rc = ffai_attn_fwd(&a, qkv, qkv + N * es, qkv + 2 * N * es, merged, attn_ws, z.attn,
+                            stream)) != FFAI_OK)
+      return rc;
+    g.b = merged; g.a = w->wo; g.d = out; g.bias = w->bo;
+    return run_gemm(h, g, dt, scratch, z.gemm, st);
+  }
   g.a = w->wq; g.d = q; g.bias = w->bq;
   if ((rc = run_gemm(h, g, dt, scratch, z.gemm, st)) != FFAI_OK) return rc;
   g.a = w->wv; g.d = v; g.bias = w->bv;
@@ -262,8 +291,6 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   gk.bias = nullptr;
   if ((rc = run_gemm(h, gk, dt, scratch, z.gemm, st)) != FFAI_OK) return rc;
   // attention: reads q, kt, v by stride and writes the merged (B, S, N) layout
-  ffai_attn_desc a;
-  attn_desc(d, &a);
   if ((rc = ffai_attn_fwd(&a, q, kt, v, merged, attn_ws, z.attn, stream)) != FFAI_OK) return rc;
   // out: (B S, N) = merged Wo^T + bo
   g.b = merged; g.a = w->wo; g.d = out; g.bias = w->bo;

@@ -19,20 +19,28 @@ from .flash_attn import _DT, _stream_handle
 
 class EncoderAttention:
     """Weights as the reference holds them: each Linear weight (out, in), each bias (out); the
-    key projection has no bias. All tensors are device tensors of one dtype (bf16 or f16)."""
+    key projection has no bias. All tensors are device tensors of one dtype (bf16 or f16).
+    `packed` (default) also packs the input projections once, [wq; wk_scaled; wv] and
+    [bq; 0; bv], so that a call runs them as one GEMM."""
 
-    def __init__(self, n_state: int, n_head: int, wq, bq, wk_scaled, wv, bv, wo, bo):
+    def __init__(self, n_state: int, n_head: int, wq, bq, wk_scaled, wv, bv, wo, bo,
+                 packed: bool = True):
         self.n_state, self.n_head = n_state, n_head
         self.w = [t.contiguous() for t in (wq, bq, wk_scaled, wv, bv, wo, bo)]
+        self.packed = None
+        if packed:
+            self.packed = (torch.cat([wq, wk_scaled, wv], 0).contiguous(),
+                           torch.cat([bq, torch.zeros_like(bq), bv], 0).contiguous())
         self._ws: Optional[torch.Tensor] = None
 
     @classmethod
-    def load(cls, n_state: int, n_head: int, wq, bq, wk, wv, bv, wo, bo) -> "EncoderAttention":
+    def load(cls, n_state: int, n_head: int, wq, bq, wk, wv, bv, wo, bo,
+             packed: bool = True) -> "EncoderAttention":
         """EncoderAttention::load: the key weight pre-scaled by head_dim^-0.5 (computed in f32,
         stored in the weights' dtype)."""
         scale = (n_state // n_head) ** -0.5
         wk_scaled = (wk.float() * scale).to(wk.dtype)
-        return cls(n_state, n_head, wq, bq, wk_scaled, wv, bv, wo, bo)
+        return cls(n_state, n_head, wq, bq, wk_scaled, wv, bv, wo, bo, packed=packed)
 
     def _desc(self, x: torch.Tensor) -> L.EncoderAttnDesc:
         d = L.EncoderAttnDesc()
@@ -59,7 +67,9 @@ class EncoderAttention:
             workspace = self._ws
         if out is None:
             out = torch.empty_like(x)
-        w = L.EncoderAttnWeights(*[t.data_ptr() for t in self.w])
+        ptrs = [t.data_ptr() for t in self.w]
+        ptrs += [t.data_ptr() for t in self.packed] if self.packed is not None else [None, None]
+        w = L.EncoderAttnWeights(*ptrs)
         L.check(L.load().ffai_encoder_attn_fwd(ctypes.byref(desc), x.data_ptr(), ctypes.byref(w),
                                                out.data_ptr(), workspace.data_ptr(),
                                                workspace.numel(), _stream_handle(x)))

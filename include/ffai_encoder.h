@@ -11,7 +11,8 @@
  * The reference splits q and v into heads with a copy each (:1103-1117) and loops over batch
  * items (:1069-1076). Here the projections land in the layouts the kernel reads by stride (no
  * copies) and the batch is one launch per GEMM: hipBLASLt GEMMs with bias epilogues (bf16/f16
- * in and out, f32 accumulation) around ffai_attn_fwd.
+ * in and out, f32 accumulation) around ffai_attn_fwd. With packed weights (wqkv, bqkv) the
+ * three input projections are one GEMM.
  *
  * All calls are asynchronous on `stream` (a hipStream_t; NULL = null stream), allocate nothing,
  * take device pointers and return FFAI_OK or a negative ffai_status (ffai_attn.h), with the
@@ -40,7 +41,11 @@ typedef struct ffai_encoder_attn_desc {
 
 /* Weights in the reference's layout: each Linear weight is (out, in) row-major, each bias
  * (out). wk_scaled is the key weight multiplied by head_dim^-0.5 once, at load
- * (EncoderAttention::load, text_decoder.rs:1039-1050); the key projection has no bias. */
+ * (EncoderAttention::load, text_decoder.rs:1039-1050); the key projection has no bias.
+ * Optionally the three input projections packed once at load: wqkv = [wq; wk_scaled; wv], one
+ * (3 n_state, n_state) row-major matrix, and bqkv = [bq; zeros(n_state); bv]. When both are
+ * set, one GEMM computes q, k and v side by side (the attention then reads K as rows) and wq,
+ * bq, wk_scaled, wv and bv are not read; otherwise those five are required. */
 typedef struct ffai_encoder_attn_weights {
   const void* wq;
   const void* bq;
@@ -49,10 +54,13 @@ typedef struct ffai_encoder_attn_weights {
   const void* bv;
   const void* wo;
   const void* bo;
+  const void* wqkv; /* optional, see above (NULL when not packed) */
+  const void* bqkv; /* optional, see above (NULL when not packed) */
 } ffai_encoder_attn_weights;
 
-/* Bytes of device workspace ffai_encoder_attn_fwd needs for `d`: q, kt, v and the merged
- * attention output in the compute dtype, the attention's own workspace, and GEMM scratch. */
+/* Bytes of device workspace ffai_encoder_attn_fwd needs for `d`, packed weights or not: q, k and
+ * v and the merged attention output in the compute dtype, the attention's own workspace, and
+ * GEMM scratch. */
 int ffai_encoder_attn_workspace_bytes(const ffai_encoder_attn_desc* d, size_t* bytes);
 
 /* x: (batch, seq, n_state) row-major; out: the same shape. workspace: at least

@@ -287,6 +287,11 @@ def test_encoder_attn_rejects_bad_arguments(lib):
     assert lib.ffai_encoder_attn_fwd(ctypes.byref(desc()), FAKE, ctypes.byref(w), FAKE, FAKE,
                                      1 << 40, None) == L.FFAI_ERR_INVALID
     assert "null" in L.last_error()
+    # a packed projection weight without its packed bias, and no separate weights either
+    w = L.EncoderAttnWeights(wqkv=FAKE, wo=FAKE, bo=FAKE)
+    assert lib.ffai_encoder_attn_fwd(ctypes.byref(desc()), FAKE, ctypes.byref(w), FAKE, FAKE,
+                                     1 << 40, None) == L.FFAI_ERR_INVALID
+    assert "wqkv" in L.last_error()
 
 
 def test_gemv_entry_points_reject_bad_arguments(lib):

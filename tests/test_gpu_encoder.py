@@ -30,11 +30,11 @@ def _case(rng, b, t, n, dt):
     return x, ws
 
 
-def _run(gpu, x, ws, n_head, dt):
+def _run(gpu, x, ws, n_head, dt, packed=True):
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu, TDT[dt])
     wq, bq, wk, wv, bv, wo, bo = ws
     ea = EncoderAttention.load(x.shape[2], n_head, dev(wq), dev(bq), dev(wk), dev(wv), dev(bv),
-                               dev(wo), dev(bo))
+                               dev(wo), dev(bo), packed=packed)
     got = ea(dev(x)).float().cpu().numpy()
     wk_s = ea.w[2].float().cpu().numpy()  # the device's pre-scaled key weight, as stored
     want = oenc.encoder_attention(x, wq, bq, wk_s, wv, bv, wo, bo, n_head, store=dt)
@@ -42,23 +42,26 @@ def _run(gpu, x, ws, n_head, dt):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_encoder_block_whisper_tiny(gpu, dt):
-    """whisper-tiny encoder layer: 6 heads x 64, n_state 384; two windows of 300 frames."""
+@pytest.mark.parametrize("packed", [True, False])
+def test_encoder_block_whisper_tiny(gpu, dt, packed):
+    """whisper-tiny encoder layer: 6 heads x 64, n_state 384; two windows of 300 frames. Packed:
+    one GEMM for q, k and v, K read as rows; unpacked: three GEMMs, K^T as the reference."""
     rng = np.random.default_rng(60)
     x, ws = _case(rng, 2, 300, 384, dt)
-    got, want = _run(gpu, x, ws, 6, dt)
+    got, want = _run(gpu, x, ws, 6, dt, packed)
     err = max_abs(got, want)
-    print(f"encoder block tiny {dt}: {err:.3e} (max |out| {np.abs(want).max():.2f})")
+    print(f"encoder block tiny {dt} packed={packed}: {err:.3e} (max |out| {np.abs(want).max():.2f})")
     assert err < TOL_BF16
 
 
-def test_encoder_block_large_v3_window(gpu):
+@pytest.mark.parametrize("packed", [True, False])
+def test_encoder_block_large_v3_window(gpu, packed):
     """whisper-large-v3 encoder layer: 20 heads x 64, n_state 1280, one 1500-frame window."""
     rng = np.random.default_rng(61)
     x, ws = _case(rng, 1, 1500, 1280, "bf16")
-    got, want = _run(gpu, x, ws, 20, "bf16")
+    got, want = _run(gpu, x, ws, 20, "bf16", packed)
     err = max_abs(got, want)
-    print(f"encoder block large-v3: {err:.3e} (max |out| {np.abs(want).max():.2f})")
+    print(f"encoder block large-v3 packed={packed}: {err:.3e} (max |out| {np.abs(want).max():.2f})")
     assert err < TOL_BF16
 
 
