@@ -637,14 +637,19 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // 2^64, and the row sums and accumulators stay finite in f32 for any realistic key count.
     // The test compares bit patterns: the build assumes no NaNs, so a float compare could be
     // folded.
+    // `redone`: the last settle redid a subtile, so the accumulator owes corr_s (wave-uniform).
+    bool redone = false;
     auto settle = [&](int st) {
-      bool bad = false;
+      // as unsigned bit patterns the lane sums (>= +0 when finite) compare above the bound
+      // exactly when too large, inf or NaN (of either sign)
+      uint32_t hi = 0u;
 #pragma unroll
       for (int c = 0; c < QW; ++c) {
         corr_s[c] = 1.f;
-        bad = bad || (__float_as_uint(rs_s[c]) & 0x7fffffffu) > __float_as_uint(kWeightSumBound);
+        hi = max(hi, __float_as_uint(rs_s[c]));
       }
-      if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+      redone = __builtin_amdgcn_ballot_w64(hi > __float_as_uint(kWeightSumBound)) != 0;
+      if (redone) {
 #pragma unroll
         for (int c = 0; c < QW; ++c) {
           const f32x16& sv = sacc[c][st];
@@ -669,10 +674,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     // Apply the rescale a redo left owing to the accumulator (whole wave, rare). Kept apart from
     // `settle`: inside its branch the accumulator would need copies on the common path.
     auto rescale = [&]() {
-      bool any = false;
-#pragma unroll
-      for (int c = 0; c < QW; ++c) any = any || corr_s[c] != 1.f;
-      if (__builtin_amdgcn_ballot_w64(any) != 0) {
+      if (redone) {
 #pragma unroll
         for (int c = 0; c < QW; ++c)
 #pragma unroll
