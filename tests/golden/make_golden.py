@@ -7,7 +7,7 @@ so these vectors are made here: seeded inputs, the oracle's output (the referenc
 restated, oracle/flash_oracle.cpp) and the float64 closed form (oracle/textbook.py) for the same
 inputs. Every case also records which reference function it exercises.
 
-Run from the repo root:  python tests/golden/make_golden.py
+Run from the repo root:  python tests/golden/make_golden.py [case names to write; default all]
 """
 
 from __future__ import annotations
@@ -93,7 +93,50 @@ def main() -> None:
         out=oracle.attend_general(q, k, v, k_transposed=False, scale=0.125, kv_lens=lens),
         f64=textbook.attention(q, k, v, scale=0.125, kv_lens=lens))
 
+    # 6. encoder f32 at the reference unit test's shape (flash_attn.rs:1005-1021: H = 4,
+    #    T = 512, scale on q), merged layout
+    rng = np.random.default_rng(7)
+    h, t = 4, 512
+    q = (rng.standard_normal((1, h, t, 64)) * 0.125).astype(np.float32)
+    kt = rng.standard_normal((1, h, 64, t)).astype(np.float32)
+    v = rng.standard_normal((1, h, t, 64)).astype(np.float32)
+    cases["encoder_f32_h4_t512"] = dict(
+        ref="MergedAttnOp at the shape of flash_attn.rs:1005-1021",
+        q=q, kt=kt, v=v, out=oracle.attend_f32(q, kt, v),
+        f64=textbook.attention(q, kt, v, k_transposed=True))
+
+    # 7. decode with f16 K/V over one 30 s window (1500 frames), 6 heads: the shipped
+    #    cross-attention arm at its real key count
+    rng = np.random.default_rng(8)
+    q = (rng.standard_normal((1, 6, 1, 64)) * 0.125).astype(np.float32)
+    kt16 = rng.standard_normal((1, 6, 64, 1500)).astype(np.float16)
+    v16 = rng.standard_normal((1, 6, 1500, 64)).astype(np.float16)
+    cases["decode_f16kv_h6_k1500"] = dict(
+        ref="FlashAttnOp f16-K/V decode arm, xattn_head_f16 (flash_attn.rs:289-356, 714-789)",
+        q=q, kt16=kt16, v16=v16, out=oracle.attend_f16kv(q, kt16, v16),
+        f64=textbook.attention(q, kt16.astype(np.float32), v16.astype(np.float32),
+                               k_transposed=True))
+
+    # 8. bf16-rounded encoder rows at the large-v3 frame count (1500; 2 heads), K transposed as
+    #    the reference's encoder produces it; outputs kept for spot rows (first, middle and
+    #    last 64) to keep the fixture small
+    rng = np.random.default_rng(9)
+    h, t = 2, 1500
+    q = oracle.round_bf16(rng.standard_normal((1, h, t, 64)).astype(np.float32))
+    kt = oracle.round_bf16(rng.standard_normal((1, h, 64, t)).astype(np.float32))
+    v = oracle.round_bf16(rng.standard_normal((1, h, t, 64)).astype(np.float32))
+    rows = np.r_[0:64, 704:768, 1436:1500].astype(np.int32)
+    full = oracle.attend_general(q, kt, v, k_transposed=True, scale=0.125)
+    f64 = textbook.attention(q, kt, v, k_transposed=True, scale=0.125)
+    cases["encoder_bf16_h2_t1500"] = dict(
+        ref="encoder attention on bf16 operands (configs 2/4 at 2 heads; extension of the f32 kernel)",
+        q_bf16=bf16_bits(q), kt_bf16=bf16_bits(kt), v_bf16=bf16_bits(v), scale=np.float32(0.125),
+        rows=rows, out=full[:, :, rows], f64=f64[:, :, rows])
+
+    only = set(sys.argv[1:])
     for name, arrays in cases.items():
+        if only and name not in only:
+            continue
         path = os.path.join(OUT, f"{name}.npz")
         ref = arrays.pop("ref")
         # the float64 closed form is stored rounded to f32 (6e-8 relative: far below any bar)

@@ -249,6 +249,10 @@ def test_golden_vectors(path):
     elif name.startswith("causal_gqa"):
         got = oracle.attend_general(_bf16(z["q_bf16"]), _bf16(z["k_bf16"]), _bf16(z["v_bf16"]),
                                     k_transposed=False, scale=float(z["scale"]), causal=True)
+    elif name.startswith("encoder_bf16"):
+        full = oracle.attend_general(_bf16(z["q_bf16"]), _bf16(z["kt_bf16"]), _bf16(z["v_bf16"]),
+                                     k_transposed=True, scale=float(z["scale"]))
+        got = full[:, :, z["rows"]]
     elif name.startswith("ragged_beams"):
         got = oracle.attend_general(_bf16(z["q_bf16"]), _bf16(z["k_bf16"]), _bf16(z["v_bf16"]),
                                     k_transposed=False, scale=float(z["scale"]),
