@@ -125,28 +125,30 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   //      then patched element by element in LDS. Every address stays inside the operand.
   // The wave's own tile, whole and aligned: global -> LDS by DMA (16-byte chunks, lane L of
   // block j fills slot L of the block; the chunk placed there is the one the swizzle assigns).
+  // A 1 KB block holds 64 / (chunks per row) whole rows, so a lane's byte offset from its
+  // block's first row changes with the block only through the chunk permutation, and the
+  // wave-uniform base moves by whole rows: offsets in 32-bit lane arithmetic (equal ones merged
+  // by the compiler), bases in scalar registers.
+  constexpr int KCH = KT ? BN / 8 : D / 8, KRB = 64 / KCH;  // K: chunks per row, rows per block
+  constexpr int VCH = D / 8, VRB = 64 / VCH;
+  const int kr = lane / KCH, kpc = lane % KCH, vr = lane / VCH, vpc = lane % VCH;
   auto dma_tile = [&](int it) {
-    const int kb = it * BN;
+    const int64_t kb = (int64_t)it * BN;
     const uint32_t kla = lds_addr(kl), vla = lds_addr(vl);
+    const char* kbase = reinterpret_cast<const char*>(kp + (KT ? kb : kb * p.k_st));
+    const char* vbase = reinterpret_cast<const char*>(vp + kb * p.v_st);
 #pragma unroll
     for (int j = 0; j < KBUF / 512; ++j) {
-      const int L = j * 64 + lane;
-      const uint16_t* src;
-      if constexpr (KT) {
-        const int r = L / (BN / 8), pc = L % (BN / 8);
-        src = kp + (int64_t)r * p.k_st + kb + 8 * swz_kt(r, pc);
-      } else {
-        const int r = L / (D / 8), pc = L % (D / 8);
-        src = kp + (int64_t)(kb + r) * p.k_st + 8 * swz_kr(r, pc);
-      }
-      lds_dma16(src, (uint32_t)__builtin_amdgcn_readfirstlane((int)(kla + j * 1024)));
+      const int r = j * KRB + kr;
+      const uint32_t off =
+          (uint32_t)(2 * (kr * p.k_st + 8 * (KT ? swz_kt(r, kpc) : swz_kr(r, kpc))));
+      lds_dma16_sbase(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
     }
 #pragma unroll
     for (int j = 0; j < VBUF / 512; ++j) {
-      const int L = j * 64 + lane;
-      const int r = L / (D / 8), pc = L % (D / 8);
-      const uint16_t* src = vp + (int64_t)(kb + r) * p.v_st + 8 * swz_v(r, pc);
-      lds_dma16(src, (uint32_t)__builtin_amdgcn_readfirstlane((int)(vla + j * 1024)));
+      const int r = j * VRB + vr;
+      const uint32_t off = (uint32_t)(2 * (vr * p.v_st + 8 * swz_v(r, vpc)));
+      lds_dma16_sbase(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
     }
   };
   // Tail tiles (past the last valid key) and misaligned K^T rows: through registers. Rows of K
