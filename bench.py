@@ -445,19 +445,20 @@ def encoder_block_bench(torch, fa, steps, warmup, layers=4, windows=16, T=1500, 
 
 def gemv_bench(torch, steps, warmup, beams=5, n=1024, layers=24, vocab=51865):
     """Every single-row projection of one decode step for all beams at once: per layer the
-    self-attention q, k, v, out and cross-attention q, out (n x n) and the MLP (4n x n, n x 4n)
-    as f16 GEMVs, then the block-scaled int8 vocabulary projection. Captured in a HIP graph.
-    Algorithmic bytes: every weight byte once (f16, int8 + block scales + corrections) plus the
-    activations read and outputs written."""
+    self-attention q, k and v (one GEMV over the three weights packed as (3n, n), since all
+    three project the same normed input), the self-attention out and cross-attention q and
+    out (n x n), and the MLP (4n x n, n x 4n) as f16 GEMVs, then the block-scaled int8
+    vocabulary projection. Captured in a HIP graph. Algorithmic bytes: every weight byte once
+    (f16, int8 + block scales + corrections) plus the activations read and outputs written."""
     from ffai_amd.gemv import F16Gemv, Int8Vocab
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(8)
-    shapes = [(n, n)] * 6 + [(4 * n, n), (n, 4 * n)]
+    shapes = [(3 * n, n)] + [(n, n)] * 3 + [(4 * n, n), (n, 4 * n)]
     mats = [[F16Gemv(torch.randn(o, i, generator=g, device=dev) / i ** 0.5) for o, i in shapes]
             for _ in range(layers)]
     xs = {i: torch.randn(beams, i, generator=g, device=dev) for i in (n, 4 * n)}
-    ys = {o: torch.empty(beams, o, device=dev) for o in (n, 4 * n)}
+    ys = {o: torch.empty(beams, o, device=dev) for o in (n, 3 * n, 4 * n)}
     iv = Int8Vocab(torch.randn(vocab, n, generator=g, device=dev) / n ** 0.5)
     logits = torch.empty(beams, vocab, device=dev)
     ws = torch.empty(iv.workspace_bytes(beams), dtype=torch.uint8, device=dev)

@@ -55,7 +55,8 @@ def test_vocab_logits_bit_exact(gpu, d, rows, vocab):
 
 
 @pytest.mark.parametrize("out_dim,in_dim,rows", [(1536, 384, 1), (1024, 1024, 5),
-                                                 (4096, 1024, 5), (1024, 4096, 9), (1023, 1280, 16)])
+                                                 (4096, 1024, 5), (1024, 4096, 9), (1023, 1280, 16),
+                                                 (3840, 1280, 5)])
 def test_gemv_f16(gpu, out_dim, in_dim, rows):
     rng = np.random.default_rng(72)
     w = rng.standard_normal((out_dim, in_dim)).astype(np.float32)
