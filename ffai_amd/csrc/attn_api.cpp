@@ -150,10 +150,14 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
   if (d->causal) kv_blk = std::min<int64_t>(kv_blk, (int64_t)d->q_offset + d->q_len);
   const int64_t n_tiles = std::max<int64_t>(1, (kv_blk + ffai::kBlockN - 1) / ffai::kBlockN);
   const int waves = d->head_dim == 64 ? 8 : 4;
-  constexpr int64_t kTargetWorkgroups = 64;
+  // Splitting costs a combine launch (~3 us), so a grid of at least kMinWorkgroups stays whole;
+  // a smaller one is split towards kSplitWorkgroups (whisper-medium cross-attention, 16 heads x
+  // 24 tiles: 10.0 us per layer at 128 workgroups, 10.9 at 64, 15.5 unsplit; the beam-5
+  // self-attention's 80 unsplit workgroups, 7.7 us, against 10.1 split in two).
+  constexpr int64_t kMinWorkgroups = 64, kSplitWorkgroups = 128;
   int64_t tps = waves;
-  if (units * ((n_tiles + tps - 1) / tps) < kTargetWorkgroups)
-    tps = std::max<int64_t>(1, n_tiles * units / kTargetWorkgroups);
+  if (units * ((n_tiles + tps - 1) / tps) < kMinWorkgroups)
+    tps = std::max<int64_t>(1, n_tiles * units / kSplitWorkgroups);
   // FFAI_DECODE_TILES_PER_WG (> 0) forces the 64-key tiles per decode workgroup: a tuning knob.
   static const int forced_tps = [] {
     const char* e = std::getenv("FFAI_DECODE_TILES_PER_WG");

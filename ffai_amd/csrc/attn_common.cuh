@@ -111,7 +111,9 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_block) {
                : "memory", "m0");
 }
 // The same with a wave-uniform 64-bit base (SGPRs) plus a per-lane 32-bit byte offset, so that
-// per tile only the scalar base moves.
+// per tile only the scalar base moves. NT marks the load non-temporal (streamed data that should
+// not displace cached lines).
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t offset,
                                                 uint32_t lds_block) {
   // the compiler cannot always prove the base uniform; the asm needs it in SGPRs
@@ -122,10 +124,23 @@ __device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t offse
   const uint64_t sb = (uint64_t)lo | ((uint64_t)hi << 32);
   base = (const void*)(uintptr_t)sb;
   lds_block = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_block);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds_block), "v"(offset), "s"(base)
-               : "memory", "m0");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                 :
+                 : "s"(lds_block), "v"(offset), "s"(base)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds_block), "v"(offset), "s"(base)
+                 : "memory", "m0");
+}
+// A wave-uniform pointer taken into scalar registers (readfirstlane of each half).
+__device__ __forceinline__ const char* uniform_ptr(const char* ptr) {
+  const uint64_t b = (uint64_t)(uintptr_t)ptr;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  return (const char*)(uintptr_t)((uint64_t)lo | ((uint64_t)hi << 32));
 }
 // s_waitcnt vmcnt(0) lgkmcnt(0): every outstanding global load (DMA included) and LDS access done.
 __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0070); }

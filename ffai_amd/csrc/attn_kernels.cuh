@@ -107,6 +107,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   const QS* qp = reinterpret_cast<const QS*>(p.q) + b * p.q_sb + h * p.q_sh;
   const KVS* kp = reinterpret_cast<const KVS*>(p.k) + b * p.k_sb + hk * p.k_sh;
   const KVS* vp = reinterpret_cast<const KVS*>(p.v) + b * p.v_sb + hk * p.v_sh;
+  const char* kp_dma = uniform_ptr(reinterpret_cast<const char*>(kp));
+  const char* vp_dma = uniform_ptr(reinterpret_cast<const char*>(vp));
 
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole key loop
   constexpr int QF = F32 ? D / 2 : D / 16;
@@ -345,9 +347,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
     if constexpr (!F32) {
       const uint32_t kl = lds_addr(k_lds + bufi * KBUF);
       const uint32_t vl = lds_addr(v_lds + bufi * VBUF);
-      const int64_t kb = (int64_t)it * BN;
-      const char* kbase = reinterpret_cast<const char*>(kp + (KT ? kb : kb * p.k_st));
-      const char* vbase = reinterpret_cast<const char*>(vp + kb * p.v_st);
+      // the tile index and the head's bases are wave-uniform: taken into scalar registers, the
+      // 64-bit address arithmetic runs on the scalar unit instead of the VALU
+      const int64_t kb = (int64_t)__builtin_amdgcn_readfirstlane(it) * BN;
+      const char* kbase = uniform_ptr(kp_dma) + 2 * (KT ? kb : kb * p.k_st);
+      const char* vbase = uniform_ptr(vp_dma) + 2 * kb * p.v_st;
 #pragma unroll
       for (int j = 0; j < KB_ / NW; ++j)
         lds_dma16_sbase(kbase, dma_koff[j], kl + (j * NW + wave) * 1024);

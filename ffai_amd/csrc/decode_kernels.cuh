@@ -142,13 +142,13 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       const int r = j * KRB + kr;
       const uint32_t off =
           (uint32_t)(2 * (kr * p.k_st + 8 * (KT ? swz_kt(r, kpc) : swz_kr(r, kpc))));
-      lds_dma16_sbase(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
+      lds_dma16_sbase<true>(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
     }
 #pragma unroll
     for (int j = 0; j < VBUF / 512; ++j) {
       const int r = j * VRB + vr;
       const uint32_t off = (uint32_t)(2 * (vr * p.v_st + 8 * swz_v(r, vpc)));
-      lds_dma16_sbase(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
+      lds_dma16_sbase<true>(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
     }
   };
   // Tail tiles (past the last valid key) and misaligned K^T rows: through registers. Rows of K
