@@ -755,10 +755,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
 
     // wave-uniform, and made visibly so, so that masking is a scalar branch rather than
     // predicated selects on every tile
+    const int q0_s = __builtin_amdgcn_readfirstlane(q0);
     auto need_mask_of = [&](int it) {
-      const int kb = it * BN;
-      return __builtin_amdgcn_readfirstlane(kb + BN > kv_end ||
-                                            (p.causal && kb + BN - 1 > p.q_offset + q0)) != 0;
+      // the tile index is taken into a scalar register first: the test is then scalar code
+      const int kb = __builtin_amdgcn_readfirstlane(it) * BN;
+      return kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset + q0_s);
     };
     auto zero_sub = [&](int st) {
 #pragma unroll
