@@ -17,7 +17,7 @@ Qwen2-VL-2B-shape causal prefill (12 query heads over 2 K/V heads, head_dim 128,
 the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this host's cores on a
 bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras] [--eager]
                        [--layers L] [--legs decode,state,block,gemv,tiny,small,prefill | none | copy]
 """
 
@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extras", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="decode leg without HIP graphs (for counter collection)")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill",
                     help="comma list of extra legs beside the headline encoder run: decode, "
@@ -151,7 +153,7 @@ def copy_bench(torch, steps, nbytes=1 << 30):
 # ------------------------------------------------------------------------------------------
 
 def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24,
-                 sets=3):
+                 sets=3, graphs=True):
     dev = torch.device("cuda:0")
     g = torch.Generator(device="cpu").manual_seed(3)
     lens_cpu = torch.randint(1, cap + 1, (layers, beams), generator=g, dtype=torch.int32)
@@ -189,25 +191,30 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
                          out=o_x.permute(2, 1, 0, 3), workspace=ws_x)
 
     # capture one HIP graph per buffer set: the step's 48 attention calls replay without
-    # host-side dispatch (the kernels use no memset; the workspaces are preallocated)
-    graphs = []
+    # host-side dispatch (the kernels use no memset; the workspaces are preallocated). Without
+    # graphs (counter collection, which serialises dispatches) every step is dispatched eagerly.
     step(all_sets[0])
     torch.cuda.synchronize()
-    for s in range(sets):
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            step(all_sets[s])
-        graphs.append(gr)
+    if graphs:
+        captured = []
+        for s in range(sets):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step(all_sets[s])
+            captured.append(gr)
+        run_step = lambda i: captured[i % sets].replay()
+    else:
+        run_step = lambda i: step(all_sets[i % sets])
     torch.cuda.synchronize()
     for i in range(warmup):
-        graphs[i % sets].replay()
+        run_step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for i in range(steps):
-        graphs[i % sets].replay()
+        run_step(i)
     e1.record(stream)
     torch.cuda.synchronize()
     gpu_ms = e0.elapsed_time(e1)
@@ -226,6 +233,7 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
         "launches_per_step": 2 * layers * 2,
         "mean_self_len": float(lens_cpu.float().mean()),
         "buffer_sets": sets,
+        "hip_graphs": graphs,
     }
 
 
@@ -547,6 +555,55 @@ def cpu_baseline(H=20, T=1500, D=64, budget_s=12.0):
     }
 
 
+def cpu_decode_baseline(beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24, reps=5):
+    """The reference's beam-5 decode step on this host, through the oracle: per layer and beam,
+    the shipped f16-K/V cross-attention arm over 1500 frames (flash_attn.rs:289-356) and the f32
+    self-attention arm over that beam's cache (:370-399; fewer than 8 keys decline there and are
+    skipped here), beams serially as decode_beam does (decoder.rs:542-596). Heads serial (the
+    reference default) and heads over the host's cores (its FFAI_PAR_HEADS arm). One layer's
+    cross-attention calls are timed and counted 24 times; every layer's self-attention is run."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    oracle.build()
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    g = torch.Generator(device="cpu").manual_seed(3)  # the GPU decode leg's cache lengths
+    lens = torch.randint(1, cap + 1, (layers, beams), generator=g, dtype=torch.int32).numpy()
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((1, H, 1, D)).astype(np.float32) * np.float32(D ** -0.5)
+    kt16 = rng.standard_normal((1, H, D, T_enc)).astype(np.float16)
+    v16 = rng.standard_normal((1, H, T_enc, D)).astype(np.float16)
+    kt_self = rng.standard_normal((1, H, D, cap)).astype(np.float32)
+    v_self = rng.standard_normal((1, H, cap, D)).astype(np.float32)
+    selfs = [(np.ascontiguousarray(kt_self[..., :n]), np.ascontiguousarray(v_self[:, :, :n]))
+             for n in sorted(set(int(x) for x in lens.ravel()))]
+    by_len = {kt.shape[3]: (kt, v) for kt, v in selfs}
+    out = {}
+    for name, par in (("heads_serial", False), ("heads_parallel", True)):
+        oracle.attend_f16kv(q, kt16, v16, par_heads=par, threads=threads)  # warm-up
+        cross = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            for _b in range(beams):
+                oracle.attend_f16kv(q, kt16, v16, par_heads=par, threads=threads)
+            cross.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        for n in lens.ravel():
+            if n >= 8:
+                kt, v = by_len[int(n)]
+                oracle.attend_f32(q, kt, v, par_heads=par, threads=threads)
+        self_s = time.perf_counter() - t0
+        out[f"us_per_step_{name}"] = (float(np.median(cross)) * layers + self_s) * 1e6
+    out["threads"] = threads
+    out["kind"] = "port"
+    out["sample"] = (f"one layer's {beams} cross-attention calls (f16 K/V, {H} heads x {T_enc} "
+                     f"frames), median of {reps}, x {layers} layers; plus all {layers * beams} "
+                     f"self-attention calls (f32 caches, the GPU leg's lengths)")
+    return out
+
+
 def load_traffic(name: str):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
@@ -582,7 +639,7 @@ def main():
     extras = {}
     if "decode" in legs:
         log("decode: beam-5 whisper-medium step ...")
-        dec = decode_bench(torch, fa, max(args.steps * 10, 100), 10)
+        dec = decode_bench(torch, fa, max(args.steps * 10, 100), 10, graphs=not args.eager)
         log(f"decode: {dec['us_per_step']:.1f} us/step, {dec['gbps']:.0f} GB/s")
         extras["decode_beam5"] = dec
     if "state" in legs:
@@ -630,6 +687,11 @@ def main():
         log("cpu baseline ...")
         cpu = cpu_baseline()
         log(f"cpu: {cpu['value'] * 1e3:.1f} GFLOP/s on {cpu['cores']} threads")
+        if "decode_beam5" in extras:
+            dcpu = cpu_decode_baseline()
+            extras["decode_beam5"]["cpu"] = dcpu
+            log(f"cpu decode step: {dcpu['us_per_step_heads_serial']:.0f} us heads serial, "
+                f"{dcpu['us_per_step_heads_parallel']:.0f} us heads parallel")
 
     achieved = enc["flop_per_launch"] / (enc["avg_launch_us"] * 1e-6) / 1e12
     line = {
