@@ -43,8 +43,10 @@ namespace {
 //   OUTT  output type. D head_dim. KT: K given transposed (d-major). NW waves per workgroup.
 //   QW    32-query column blocks per wave.
 // ---------------------------------------------------------------------------------------------
+// Four-wave launches are built for two workgroups per CU (<= 256 VGPRs): the second wave on each
+// SIMD is what hides the first one's exp and dependency latencies.
 template <int MODE, int KVT, int OUTT, int D, bool KT, int NW, int QW>
-__global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2 : 1) void fwd_kernel(FwdParams p) {
   constexpr int NT = NW * 64;
   constexpr bool F32 = (MODE == kF32);
   using LT = std::conditional_t<F32, float, uint16_t>;  // LDS / compute storage type
@@ -65,11 +67,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   constexpr int VROW = F32 ? BN + 4 : D;
   constexpr int KBUF = (!F32 && KT) ? D * KTROW : BN * KROW;
   constexpr int VBUF = F32 ? D * VROW : BN * VROW;
-  // f32: double-buffered, one barrier per tile at the tile's end. 16-bit: three buffers, so the
-  // next tile can be staged and published (barrier) before the current tile's last product, and
-  // that product overlaps the next tile's first one.
-  constexpr int NBUF = F32 ? 2 : 3;
-  __shared__ __attribute__((aligned(16))) LT k_lds[NBUF * KBUF];
+  // f32: double-buffered, one barrier per tile at the tile's end. 16-bit: the next tile is
+  // staged and published (barrier) before the current tile's last product, so that product
+  // overlaps the next tile's first one. Tile i's K is last read before the barrier of tile i,
+  // its V after it (the last product): when that barrier stages tile i + 2, K(i + 2) can take
+  // K(i)'s buffer but V(i + 2) needs a third. Head_dim 128 keeps two K buffers (80 KB of LDS:
+  // two workgroups per CU); head_dim 64 keeps three of each (48 KB, as measured).
+  constexpr int NBUF = F32 ? 2 : 3;                    // V buffers
+  constexpr int NBK = F32 ? 2 : (D == 128 ? 2 : 3);  // K buffers
+  __shared__ __attribute__((aligned(16))) LT k_lds[NBK * KBUF];
   __shared__ __attribute__((aligned(16))) LT v_lds[NBUF * VBUF];
 
   // ---- which (batch, head, query block, key split) this workgroup computes
@@ -257,9 +263,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   // Write the tile `it` held in kreg/vreg to LDS buffer `buf`. Rows past the last valid key
   // (they were loaded from the clamped address) are zeroed here rather than at load time, so
   // that nothing waits for the loads until the tile is stored, one iteration later.
-  auto store_tile = [&](int buf, int it) {
-    LT* kl = k_lds + buf * KBUF;
-    LT* vl = v_lds + buf * VBUF;
+  auto store_tile = [&](int kbuf, int vbuf, int it) {
+    LT* kl = k_lds + kbuf * KBUF;
+    LT* vl = v_lds + vbuf * VBUF;
     const int kb = it * BN;
     const int klast = kv_end - 1;
     const bool full = kb + BN <= kv_end;
@@ -343,10 +349,10 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       dma_voff[j] = (uint32_t)(2 * ((int64_t)r * p.v_st + 8 * swz_v(r, pc)));
     }
   }
-  auto dma_tile = [&](int bufi, int it) {
+  auto dma_tile = [&](int kbuf, int vbuf, int it) {
     if constexpr (!F32) {
-      const uint32_t kl = lds_addr(k_lds + bufi * KBUF);
-      const uint32_t vl = lds_addr(v_lds + bufi * VBUF);
+      const uint32_t kl = lds_addr(k_lds + kbuf * KBUF);
+      const uint32_t vl = lds_addr(v_lds + vbuf * VBUF);
       // the tile index and the head's bases are wave-uniform: taken into scalar registers, the
       // 64-bit address arithmetic runs on the scalar unit instead of the VALU
       const int64_t kb = (int64_t)__builtin_amdgcn_readfirstlane(it) * BN;
@@ -360,14 +366,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
         lds_dma16_sbase(vbase, dma_voff[j], vl + (j * NW + wave) * 1024);
     }
   };
-  // Stage tile `it` into buffer `bufi`: by DMA when whole and aligned, else through registers
-  // (clamped, zero-filled tail; element-wise loads when misaligned), synchronously.
-  auto stage_tile = [&](int bufi, int it) {
+  // Stage tile `it` into K buffer `kbuf` and V buffer `vbuf`: by DMA when whole and aligned,
+  // else through registers (clamped, zero-filled tail; element-wise loads when misaligned),
+  // synchronously.
+  auto stage_tile = [&](int kbuf, int vbuf, int it) {
     if (p.dma && it * BN + BN <= kv_end) {
-      dma_tile(bufi, it);
+      dma_tile(kbuf, vbuf, it);
     } else {
       load_tile(it);
-      store_tile(bufi, it);
+      store_tile(kbuf, vbuf, it);
     }
   };
 
@@ -391,11 +398,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
   if (t_begin < t_end) {
     if constexpr (F32) {
       load_tile(t_begin);
-      store_tile(0, t_begin);
+      store_tile(0, 0, t_begin);
       if (t_begin + 1 < t_end) load_tile(t_begin + 1);
     } else {
-      stage_tile(0, t_begin);
-      if (t_begin + 1 < t_end) stage_tile(1, t_begin + 1);
+      stage_tile(0, 0, t_begin);
+      if (t_begin + 1 < t_end) stage_tile(1, 1, t_begin + 1);
       vm_wait_all();
     }
   }
@@ -481,7 +488,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
               oacc[0][dt] = mfma_f32(a[e], sacc[0][st][4 * j + e], oacc[0][dt]);
           }
       if (it + 1 < t_end) {
-        store_tile(buf ^ 1, it + 1);
+        store_tile(buf ^ 1, buf ^ 1, it + 1);
         if (it + 2 < t_end) load_tile(it + 2);
       }
       __syncthreads();
@@ -790,9 +797,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       }
     }
     for (int it = t_begin; it < t_end; ++it) {
-      const int buf = (it - t_begin) % NBUF;
-      const LT* kl = k_lds + buf * KBUF;
-      const LT* vl = v_lds + buf * VBUF;
+      const LT* kl = k_lds + ((it - t_begin) % NBK) * KBUF;
+      const LT* vl = v_lds + ((it - t_begin) % NBUF) * VBUF;
       const int kb = it * BN;
       const bool need_mask = need_mask_of(it);
       zero_sub(1);
@@ -815,15 +821,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && D == 64) ? 2 : 1) void fwd_ker
       // stage tile it + 2 into the buffer of tile it - 1, which every wave has finished with
       // once it passes this barrier.
       const bool more = it + 1 < t_end;
-      const int nbuf = (it + 1 - t_begin) % NBUF;
+      const int nkbuf = (it + 1 - t_begin) % NBK;
       vm_wait_all();
       __syncthreads();
-      if (it + 2 < t_end) stage_tile((it + 2 - t_begin) % NBUF, it + 2);
+      if (it + 2 < t_end) stage_tile((it + 2 - t_begin) % NBK, (it + 2 - t_begin) % NBUF, it + 2);
       // D: O^T += V^T P^T for subtile 1, and S^T of the next tile's subtile 0
       pv(vl, 1);
       if (more) {
         zero_sub(0);
-        qk(sacc, k_lds + nbuf * KBUF, 0);
+        qk(sacc, k_lds + nkbuf * KBUF, 0);
         if (need_mask_of(it + 1)) mask_subtile(sacc, (it + 1) * BN, 0);
       }
     }
