@@ -169,7 +169,9 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
   const int64_t max_splits = std::max<int64_t>(1, ffai::kCombineLdsFloats / (rows * (d->head_dim + 2)));
   if ((n_tiles + tps - 1) / tps > max_splits) tps = (n_tiles + max_splits - 1) / max_splits;
   p->decode = true;
-  p->waves = waves;
+  // a split of at most four tiles runs on four waves: half the merge through LDS (beam-5
+  // whisper-medium step: 442 -> 438 us)
+  p->waves = (d->head_dim == 64 && tps <= 4) ? 4 : waves;
   p->variant = 0;
   p->n_qblk = 1;
   p->tiles_per_split = (int)tps;
