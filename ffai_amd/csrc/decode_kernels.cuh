@@ -218,9 +218,19 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     if (!has) continue;
     // the tile region is this wave's own: reuse needs only its own earlier LDS reads done
     if (i > 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    if (kb + BN <= kv_end) dma_tile(it);
+    // A ragged tail that still lies inside the operand's rows (a per-beam cache shorter than
+    // its capacity) comes by DMA too. Its keys past the end are masked below, but their V rows
+    // may hold anything (inf, NaN) and a masked weight of 0 times NaN is NaN: they are cleared
+    // in LDS once the DMA has landed.
+    const bool tail_dma = kb + BN > kv_end && kb + BN <= p.Tk;
+    if (kb + BN <= kv_end || tail_dma) dma_tile(it);
     else stage_tile(it);
     vm_wait_all();
+    if (tail_dma) {
+      constexpr int RU = D / 8;  // 16-byte units per V row; the swizzle stays within a row
+      for (int u = max(0, kv_end - kb) * RU + lane; u < BN * RU; u += 64)
+        *reinterpret_cast<u32x4*>(&vl[8 * u]) = u32x4{0u, 0u, 0u, 0u};
+    }
 
     // ---- S^T for the tile's two 32-key subtiles: sacc[st][r] <-> key kb + 32st + 8(r/4) +
     //      4g + r%4 of row n32

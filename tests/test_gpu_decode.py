@@ -100,6 +100,32 @@ def test_ragged_caches_with_empty_one(gpu):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("k_transposed", [False, True])
+def test_ragged_caches_with_garbage_past_the_end(gpu, k_transposed):
+    """Cache rows past each beam's length hold inf and NaN (stale or never written): a tail tile
+    inside the cache's capacity arrives whole by DMA and only the valid keys may count."""
+    rng = np.random.default_rng(8)
+    beams, h, cap, d = 5, 4, 448, 64
+    lens = np.array([1, 63, 100, 383, 447], np.int32)
+    q = round_bf16(randn(rng, (beams, h, 1, d)))
+    k = round_bf16(randn(rng, (beams, h, cap, d)))
+    v = round_bf16(randn(rng, (beams, h, cap, d)))
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=0.125, kv_lens=lens)
+    for bi, n in enumerate(lens):
+        k[bi, :, n:] = np.nan
+        v[bi, :, n:: 2] = np.inf
+        v[bi, :, n + 1:: 2] = np.nan
+    kd = _dev(np.swapaxes(k, 2, 3) if k_transposed else k, torch.bfloat16, gpu)
+    out = fa.attention(_dev(q, torch.bfloat16, gpu), kd, _dev(v, torch.bfloat16, gpu),
+                       k_transposed=k_transposed, scale=0.125,
+                       kv_lens=torch.from_numpy(lens).to(gpu), out_dtype=torch.float32)
+    got = _host(out)
+    assert np.isfinite(got).all()
+    err = max_abs(got, want)
+    print(f"ragged with garbage past the end (k_transposed={k_transposed}): {err:.3e}")
+    assert err < TOL_BF16
+
+
 def test_unaligned_operands(gpu):
     """Operands offset by one element from 16-byte boundaries take the element-wise loads."""
     rng = np.random.default_rng(5)
