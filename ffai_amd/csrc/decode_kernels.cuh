@@ -151,6 +151,54 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       lds_dma16_sbase<true>(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
     }
   };
+  // The operand's last tile, when it has at least 8 keys but fewer than 64 (cross-attention over
+  // 1500 frames): DMA as well, each lane's source clamped inside the operand. K/V rows past the
+  // last valid key read that key's row instead; K^T 8-key chunks that would cross the
+  // operand's end read the tile's first chunk. The slots of masked keys then hold finite
+  // stand-ins; the valid keys of the one K^T chunk that crosses the end are patched afterwards.
+  auto dma_tile_clamped = [&](int it) {
+    const int kb = it * BN;
+    const int klast = kv_end - 1;
+    const uint32_t kla = lds_addr(kl), vla = lds_addr(vl);
+    const char* kbase = reinterpret_cast<const char*>(kp + (KT ? kb : (int64_t)kb * p.k_st));
+    const char* vbase = reinterpret_cast<const char*>(vp + (int64_t)kb * p.v_st);
+#pragma unroll
+    for (int j = 0; j < KBUF / 512; ++j) {
+      const int r = j * KRB + kr;
+      if constexpr (KT) {
+        const int c0 = kb + 8 * swz_kt(r, kpc);
+        const int src = c0 + 8 <= p.Tk ? c0 : kb;
+        const uint32_t off = (uint32_t)(2 * (kr * p.k_st + (src - kb)));
+        lds_dma16_sbase<true>(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
+      } else {
+        const int key = min(kb + r, klast);
+        const uint32_t off = (uint32_t)(2 * ((key - kb) * p.k_st + 8 * swz_kr(r, kpc)));
+        lds_dma16_sbase<true>(kbase, off, kla + j * 1024);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VBUF / 512; ++j) {
+      const int r = j * VRB + vr;
+      const int key = min(kb + r, klast);
+      const uint32_t off = (uint32_t)(2 * ((key - kb) * p.v_st + 8 * swz_v(r, vpc)));
+      lds_dma16_sbase<true>(vbase, off, vla + j * 1024);
+    }
+  };
+  // After a clamped K^T DMA has landed: the valid keys of the 8-key chunk that crosses the
+  // operand's end, element by element.
+  auto patch_kt_end = [&](int it) {
+    const int kb = it * BN;
+    const int klast = kv_end - 1;
+    const int s0 = klast & ~7;
+    if (s0 + 8 <= p.Tk) return;  // that chunk was read whole
+    for (int d = lane; d < D; d += 64) {
+      const uint16_t* row = kp + (int64_t)d * p.k_st;
+      for (int k = s0; k <= klast; ++k) {
+        const int col = k - kb;
+        kl[d * KTROW + 8 * swz_kt(d, col >> 3) + (col & 7)] = row[k];
+      }
+    }
+  };
   // Tail tiles (past the last valid key) and misaligned K^T rows: through registers. Rows of K
   // and V: 16-byte units, the key index clamped to the last valid key and zeroed past it. K^T
   // rows: 4-key (8-byte) chunks, each loaded when all four keys are valid and zeroed otherwise;
@@ -223,10 +271,15 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     // may hold anything (inf, NaN) and a masked weight of 0 times NaN is NaN: they are cleared
     // in LDS once the DMA has landed.
     const bool tail_dma = kb + BN > kv_end && kb + BN <= p.Tk;
+    const bool end_dma = kb + BN > p.Tk && kb + 8 <= p.Tk;
     if (kb + BN <= kv_end || tail_dma) dma_tile(it);
+    else if (end_dma) dma_tile_clamped(it);
     else stage_tile(it);
     vm_wait_all();
-    if (tail_dma) {
+    if constexpr (KT) {
+      if (end_dma) patch_kt_end(it);
+    }
+    if (tail_dma || end_dma) {
       constexpr int RU = D / 8;  // 16-byte units per V row; the swizzle stays within a row
       for (int u = max(0, kv_end - kb) * RU + lane; u < BN * RU; u += 64)
         *reinterpret_cast<u32x4*>(&vl[8 * u]) = u32x4{0u, 0u, 0u, 0u};

@@ -126,6 +126,32 @@ def test_ragged_caches_with_garbage_past_the_end(gpu, k_transposed):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("d,k_transposed,tk,cut", [(64, True, 1500, 0), (64, True, 1500, 3),
+                                                   (64, True, 1484, 0), (64, False, 1503, 2),
+                                                   (128, True, 1500, 5), (128, False, 72, 0),
+                                                   (64, True, 72, 1)])
+def test_last_tile_past_the_operand_end(gpu, d, k_transposed, tk, cut):
+    """The operand's last tile holds fewer than 64 keys (1500 frames: 28): it arrives by DMA with
+    sources clamped inside the operand, and the valid keys of the K^T chunk that crosses the end
+    are patched. `cut` > 0 ends the valid keys (kv_lens) inside that tile, short of the end."""
+    rng = np.random.default_rng(tk + d)
+    rows, h = 5, 4
+    q = round_bf16(randn(rng, (1, h, rows, d)))
+    k = round_bf16(randn(rng, (1, h, tk, d)))
+    v = round_bf16(randn(rng, (1, h, tk, d)))
+    lens = np.array([tk - cut], np.int32)
+    kd = _dev(np.swapaxes(k, 2, 3) if k_transposed else k, torch.bfloat16, gpu)
+    out = fa.attention(_dev(q, torch.bfloat16, gpu), kd, _dev(v, torch.bfloat16, gpu),
+                       k_transposed=k_transposed, scale=d ** -0.5,
+                       kv_lens=torch.from_numpy(lens).to(gpu) if cut else None,
+                       out_dtype=torch.float32)
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=d ** -0.5,
+                                 kv_lens=lens if cut else None)
+    err = max_abs(_host(out), want)
+    print(f"last tile past the end d{d} kt{int(k_transposed)} tk{tk} cut{cut}: {err:.3e}")
+    assert err < TOL_BF16
+
+
 def test_unaligned_operands(gpu):
     """Operands offset by one element from 16-byte boundaries take the element-wise loads."""
     rng = np.random.default_rng(5)
