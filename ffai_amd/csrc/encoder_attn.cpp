@@ -251,7 +251,7 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   void* scratch = ws + z.q + z.kt + z.v + z.merged + z.attn;
   const hipDataType dt = d->dtype == FFAI_BF16 ? HIP_R_16BF : HIP_R_16F;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t BS = (int64_t)d->batch * d->seq, S = d->seq, N = d->n_state;
+  const int64_t BS = (int64_t)d->batch * d->seq, N = d->n_state;
 
   // q, v: (B S, N) = x W^T + b  ->  D^T (N x BS) = W (op T) * x^T
   Gemm g{};

@@ -17,93 +17,19 @@
 namespace ffai {
 namespace {
 
-// ---- f16 GEMV -------------------------------------------------------------------------------
-// Fallback (every beam's x too large for LDS): one wave per 4 output rows. Lane l multiplies 8-element chunks l, l + 64, ... of each of its
-// rows' weights (16-byte loads, coalesced along the row) with every beam's x, then the wave
-// reduces each (row, beam) sum.
-constexpr int kGemvRowsPerWave = 4;
-
-// R: beam rows the kernel is built for (>= rows, the rows actually present).
+// ---- f16 GEMV ---------------------------------------------------------------------------------
+// A workgroup of 4 waves, one output row per wave: lane l takes the row's 16-byte weight chunks
+// l, l + 64, ... (coalesced along the row, four in flight per lane), widens them to f32 and
+// multiplies them with every beam's x, read straight from global memory (the few KB of x stay
+// in L2; staging them in LDS behind a barrier put a second dependent round trip in front of the
+// weight loads), then the wave reduces each beam's sum.
 template <int R>
-__global__ __launch_bounds__(64) void gemv_f16_kernel(const uint16_t* __restrict__ w, int out_dim,
-                                                      int in_dim, const float* __restrict__ x,
-                                                      int rows, int64_t xs, float* __restrict__ y,
-                                                      int64_t ys) {
-  const int lane = threadIdx.x;
-  const int o0 = blockIdx.x * kGemvRowsPerWave;
-  float acc[kGemvRowsPerWave][R];
-#pragma unroll
-  for (int i = 0; i < kGemvRowsPerWave; ++i)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[i][r] = 0.f;
-  const int chunks = in_dim / 8;
-  for (int c = lane; c < chunks; c += 64) {
-    float xv[R][8];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int rr = min(r, rows - 1);  // rows past `rows` repeat the last; never stored
-      const f32x4 a = *reinterpret_cast<const f32x4*>(x + rr * xs + 8 * c);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(x + rr * xs + 8 * c + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xv[r][e] = a[e], xv[r][4 + e] = b[e];
-    }
-#pragma unroll
-    for (int i = 0; i < kGemvRowsPerWave; ++i) {
-      const int o = min(o0 + i, out_dim - 1);
-      const u32x4 wv = ld16(w + (int64_t)o * in_dim + 8 * c);
-      float wf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        wf[2 * e] = to_f32<kF16>(wv[e] & 0xffffu);
-        wf[2 * e + 1] = to_f32<kF16>(wv[e] >> 16);
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][r] = __builtin_fmaf(wf[e], xv[r][e], acc[i][r]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kGemvRowsPerWave; ++i)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float v = acc[i][r];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-      if (lane == i * R + r && r < rows && o0 + i < out_dim) y[r * ys + o0 + i] = v;
-    }
-}
-
-template <int R>
-hipError_t launch_gemv(const uint16_t* w, int out_dim, int in_dim, const float* x, int rows,
-                       int64_t xs, float* y, int64_t ys, hipStream_t st) {
-  const unsigned grid = (unsigned)((out_dim + kGemvRowsPerWave - 1) / kGemvRowsPerWave);
-  hipLaunchKernelGGL((gemv_f16_kernel<R>), dim3(grid), dim3(64), 0, st, w, out_dim, in_dim, x,
-                     rows, xs, y, ys);
-  return hipGetLastError();
-}
-
-// x staged in LDS: a workgroup of 4 waves stages every beam's x once (R * in_dim f32, at most
-// kGemvLdsBytes), then each wave computes one output row: lane l takes 8-element chunks l, l + 64,
-// ... of the row, four weight chunks in flight at a time.
-constexpr int kGemvLdsBytes = 64 * 1024;
-
-template <int R>
-__global__ __launch_bounds__(256) void gemv_f16_lds_kernel(const uint16_t* __restrict__ w,
-                                                           int out_dim, int in_dim,
-                                                           const float* __restrict__ x, int rows,
-                                                           int64_t xs, float* __restrict__ y,
-                                                           int64_t ys) {
-  extern __shared__ float x_lds[];  // [R][in_dim]
+__global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restrict__ w,
+                                                       int out_dim, int in_dim,
+                                                       const float* __restrict__ x, int rows,
+                                                       int64_t xs, float* __restrict__ y,
+                                                       int64_t ys) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n4 = in_dim / 4;
-  for (int i = tid; i < R * n4; i += 256) {
-    const int r = i / n4, k = i - r * n4;
-    const int rr = min(r, rows - 1);  // rows past `rows` repeat the last; never stored
-    *reinterpret_cast<f32x4*>(x_lds + r * in_dim + 4 * k) =
-        *reinterpret_cast<const f32x4*>(x + rr * xs + 4 * k);
-  }
-  __syncthreads();
   const int o = blockIdx.x * 4 + wave;
   if (o >= out_dim) return;
   const uint16_t* wr = w + (int64_t)o * in_dim;
@@ -131,8 +57,10 @@ __global__ __launch_bounds__(256) void gemv_f16_lds_kernel(const uint16_t* __res
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(x_lds + r * in_dim + 8 * c);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(x_lds + r * in_dim + 8 * c + 4);
+        // beams past `rows` repeat the last one's x (R is the compiled width); never stored
+        const float* xr = x + min(r, rows - 1) * xs + 8 * c;
+        const f32x4 a = *reinterpret_cast<const f32x4*>(xr);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(xr + 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           acc[r] = __builtin_fmaf(wf[e], a[e], acc[r]);
@@ -153,14 +81,10 @@ __global__ __launch_bounds__(256) void gemv_f16_lds_kernel(const uint16_t* __res
 template <int R>
 hipError_t launch_gemv_any(const uint16_t* w, int out_dim, int in_dim, const float* x, int rows,
                            int64_t xs, float* y, int64_t ys, hipStream_t st) {
-  const size_t lds = (size_t)R * in_dim * sizeof(float);
-  if (lds <= kGemvLdsBytes) {
-    const unsigned grid = (unsigned)((out_dim + 3) / 4);
-    hipLaunchKernelGGL((gemv_f16_lds_kernel<R>), dim3(grid), dim3(256), lds, st, w, out_dim,
-                       in_dim, x, rows, xs, y, ys);
-    return hipGetLastError();
-  }
-  return launch_gemv<R>(w, out_dim, in_dim, x, rows, xs, y, ys, st);
+  const unsigned grid = (unsigned)((out_dim + 3) / 4);
+  hipLaunchKernelGGL((gemv_f16_kernel<R>), dim3(grid), dim3(256), 0, st, w, out_dim,
+                     in_dim, x, rows, xs, y, ys);
+  return hipGetLastError();
 }
 
 // ---- int8 vocabulary projection -------------------------------------------------------------
