@@ -873,44 +873,45 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   }
 }
 
-// Merge split-key partials by log-sum-exp: one 64-lane workgroup per (batch, head, query row).
-// Partial maxima are in scaled log2 units.
+// Merge split-key partials by log-sum-exp. D/4 lanes per (batch, head, query row), four elements
+// each, so a 256-thread workgroup merges 1024/D rows (one workgroup per row spent the launch on
+// dispatch: 30000 workgroups for one whisper-large-v3 window). Partial maxima are in scaled log2
+// units.
 template <int OUTT, int D>
-__global__ __launch_bounds__(64) void combine_kernel(CombineParams p) {
-  const int row = blockIdx.x;
+__global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
+  constexpr int LPR = D / 4, RPB = 256 / LPR;
+  const int rows = p.B * p.Hq * p.Tq;
+  const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+  if (row >= rows) return;
+  const int c4 = threadIdx.x % LPR;  // this lane's 4 elements: 4 c4 .. 4 c4 + 3
   const int t = row % p.Tq;
   const int bh = row / p.Tq;
   const int h = bh % p.Hq, b = bh / p.Hq;
   const int64_t base = (int64_t)bh * p.n_split * p.Tq + t;  // partial row of split 0
-  const float* wo = p.ws + base * D;
+  const float* wo = p.ws + base * D + 4 * c4;
   const float* ml = p.ws + (int64_t)p.B * p.Hq * p.n_split * p.Tq * D + base * 2;
   const int64_t so = (int64_t)p.Tq * D, sml = (int64_t)p.Tq * 2;
-  // every lane loads one split's (m, l) so the loads are issued together
-  const int lane = threadIdx.x;
   float m = kNegInf;
-  for (int s = lane; s < p.n_split; s += 64) m = fmaxf(m, ml[s * sml]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+#pragma unroll 4
+  for (int s = 0; s < p.n_split; ++s) m = fmaxf(m, ml[s * sml]);
   const float mu = (m == kNegInf) ? 0.f : m;
-  constexpr int PER = D / 64;
-  float acc[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) acc[i] = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
+#pragma unroll 4
   for (int s = 0; s < p.n_split; ++s) {
-    const float w = fast_exp2(ml[s * sml] - mu);
-    l = __builtin_fmaf(w, ml[s * sml + 1], l);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) acc[i] = __builtin_fmaf(w, wo[s * so + lane + 64 * i], acc[i]);
+    const f32x2 ms = *reinterpret_cast<const f32x2*>(ml + s * sml);
+    const float w = fast_exp2(ms[0] - mu);  // 0 for an empty split (m = -inf)
+    l = __builtin_fmaf(w, ms[1], l);
+    acc += w * *reinterpret_cast<const f32x4*>(wo + s * so);
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  store_t<OUTT>* op =
-      reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh + (int64_t)t * p.o_st;
+  store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
+                      (int64_t)t * p.o_st + 4 * c4;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const float x = acc[i] * inv;
-    if constexpr (OUTT == kF32) op[lane + 64 * i] = x;
-    else op[lane + 64 * i] = from_f32<OUTT>(x);
+  for (int e = 0; e < 4; ++e) {
+    const float x = acc[e] * inv;
+    if constexpr (OUTT == kF32) op[e] = x;
+    else op[e] = from_f32<OUTT>(x);
   }
 }
 

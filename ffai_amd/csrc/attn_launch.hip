@@ -19,9 +19,10 @@ hipError_t launch_fwd(const FwdParams& p, int mode, int kv_dtype, int out_dtype,
 
 hipError_t launch_combine(const CombineParams& p, int out_dtype, int head_dim,
                           hipStream_t stream) {
-  const dim3 grid((unsigned)(p.B * p.Hq * p.Tq));
-#define FFAI_COMBINE(OT, DD) \
-  hipLaunchKernelGGL((combine_kernel<OT, DD>), grid, dim3(64), 0, stream, p)
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Tq;
+#define FFAI_COMBINE(OT, DD)                                                                  \
+  hipLaunchKernelGGL((combine_kernel<OT, DD>), dim3((unsigned)((rows + 1024 / DD - 1) / (1024 / DD))), \
+                     dim3(256), 0, stream, p)
   if (head_dim == 64) {
     if (out_dtype == kF32) FFAI_COMBINE(kF32, 64);
     else if (out_dtype == kBF16) FFAI_COMBINE(kBF16, 64);
