@@ -220,7 +220,17 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok) {
   const int64_t waves = work * (p.variant == ffai::kWave1 ? 1 : 4);
   int64_t want = 1;
   if (f32) want = (4096 + waves - 1) / waves;
-  else if (work < 256) want = (512 + work - 1) / work;
+  // Four-wave grids under 256 workgroups split the keys in three: one window of whisper
+  // tiny/small/medium/large-v3 (72-240 workgroups) measured best at 3 splits (tiny 20.2 us
+  // against 24.5 at 8, small 28.5 against 30.4 at 4; more splits cost combine traffic). One-wave
+  // grids (prompt steps) keep about 512 workgroups.
+  else if (work < 256) want = p.variant == ffai::kWave1 ? (512 + work - 1) / work : 3;
+  // FFAI_ATTN_SPLITS (> 0) forces the key splits of a fwd launch: a tuning knob.
+  static const int forced_splits = [] {
+    const char* e = std::getenv("FFAI_ATTN_SPLITS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced_splits > 0) want = forced_splits;
   if (allow_split && want > 1 && n_tiles >= 2) {
     want = std::min<int64_t>(want, n_tiles);
     p.tiles_per_split = (int)((n_tiles + want - 1) / want);
