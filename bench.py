@@ -616,9 +616,9 @@ def load_traffic(name: str):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
-              f"{args.gpus}). The attention shards over (batch, head) with no exchange; see "
-              f"DESIGN.md.", file=sys.stderr)
+        print(f"bench.py measures one GPU: there is no multi-GPU path (asked for {args.gpus}). "
+              f"The attention shards over (batch, head) with no exchange, so N GPUs would each "
+              f"run this benchmark's kernels on their share of the heads.", file=sys.stderr)
         sys.exit(2)
     import torch
 
