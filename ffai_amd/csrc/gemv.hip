@@ -11,11 +11,30 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.cuh"
 
 namespace ffai {
 namespace {
+
+// Sum over the wave's 64 lanes in VALU cross-lane moves (DPP), no LDS permutes: within each
+// 16-lane row by quad permutes and row rotations, then rows 0-3 folded into lane 63 by the row
+// broadcasts of lanes 15 and 31 (lanes without a source add 0); the total is read from lane 63.
+__device__ __forceinline__ float dpp_add(float v, int x) { return v + __builtin_bit_cast(float, x); }
+__device__ __forceinline__ float wave_sum(float v) {
+  auto mv = [](float a, auto ctrl) {
+    return __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), decltype(ctrl)::value, 0xf,
+                                       0xf, false);
+  };
+  v = dpp_add(v, mv(v, std::integral_constant<int, 0xb1>{}));   // quad_perm [1,0,3,2]
+  v = dpp_add(v, mv(v, std::integral_constant<int, 0x4e>{}));   // quad_perm [2,3,0,1]
+  v = dpp_add(v, mv(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+  v = dpp_add(v, mv(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
+  v = dpp_add(v, mv(v, std::integral_constant<int, 0x142>{}));  // row_bcast:15
+  v = dpp_add(v, mv(v, std::integral_constant<int, 0x143>{}));  // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 
 // ---- f16 GEMV ---------------------------------------------------------------------------------
 // A workgroup of 4 waves, one output row per wave: lane l takes the row's 16-byte weight chunks
@@ -71,9 +90,7 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restric
   }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float v = acc[r];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    const float v = wave_sum(acc[r]);
     if (lane == r && r < rows) y[r * ys + o] = v;
   }
 }
