@@ -107,6 +107,7 @@ def load():
     L.ffai_attn_serves.argtypes = [dp]
     L.ffai_attn_workspace_bytes.argtypes = [dp, ctypes.POINTER(sz)]
     L.ffai_attn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
+    L.ffai_attn_plan_info.argtypes = [dp, ctypes.POINTER(ctypes.c_int32)]
     L.ffai_serves.argtypes = [tp, tp]
     L.ffai_attend.argtypes = [tp, tp, tp, ctypes.c_int, tp, vp, sz, vp]
     L.ffai_attend_workspace_bytes.argtypes = [tp, tp, tp, ctypes.POINTER(sz)]
@@ -129,7 +130,8 @@ def load():
     L.ffai_vocab_int8_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_vocab_int8_logits.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, i64, vp,
                                          ctypes.c_size_t, vp]
-    for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd", "ffai_serves",
+    for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd",
+                 "ffai_attn_plan_info", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
                  "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",
@@ -138,6 +140,16 @@ def load():
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
+
+
+def plan_info(desc: AttnDesc) -> dict:
+    """The launch plan ffai_attn_fwd uses for `desc` with vector-aligned operands."""
+    info = (ctypes.c_int32 * 5)()
+    check(load().ffai_attn_plan_info(ctypes.byref(desc), info))
+    kernel = "decode" if info[0] == 1 else "fwd"
+    shape = info[1] if kernel == "decode" else ("wave1", "wave4", "wave4x2")[info[1]]
+    return {"kernel": kernel, "shape": shape, "splits": info[2], "tiles_per_split": info[3],
+            "workgroups": info[4]}
 
 
 def last_error() -> str:

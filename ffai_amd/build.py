@@ -37,9 +37,10 @@ def flags() -> list[str]:
         "-O3", "-std=c++17", "-fPIC",
         f"--offload-arch={ARCH}",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # No NaN is ever produced or consumed (masked scores are -inf, never NaN): let maxima
-        # skip IEEE NaN quieting (otherwise every fmaxf operand is canonicalised first).
-        "-fno-honor-nans", "-mno-amdgpu-ieee",
+        # No NaN is ever produced or consumed in the kernels (masked scores are -inf, never
+        # NaN): let maxima skip IEEE NaN quieting (otherwise every fmaxf operand is canonicalised
+        # first). Device code only: the host-side argument checks must still see a NaN as NaN.
+        "-Xarch_device", "-fno-honor-nans", "-Xarch_device", "-mno-amdgpu-ieee",
         "-I", os.path.join(ROOT, "include"),
         "-Wall", "-Wno-unused-function",
     ]

@@ -459,6 +459,21 @@ int ffai_attn_fwd(const ffai_attn_desc* d, const void* q, const void* k, const v
   return run_fwd(d, q, k, v, out, workspace, workspace_bytes, stream, true);
 }
 
+int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]) {
+  if (!info) return fail(FFAI_ERR_INVALID, "null info pointer");
+  std::string why;
+  const int rc = check_desc(d, &why);
+  if (rc == FFAI_DECLINED) return fail(FFAI_DECLINED, "declined: " + why);
+  if (rc != FFAI_OK) return fail(rc, why);
+  const Plan p = make_plan(d, true, true);
+  info[0] = p.decode ? 1 : 0;
+  info[1] = p.decode ? p.waves : p.variant;
+  info[2] = p.n_split;
+  info[3] = p.tiles_per_split;
+  info[4] = p.n_work;
+  return FFAI_OK;
+}
+
 int ffai_serves(const ffai_tensor* kt, const ffai_tensor* v) {
   if (!kt || !v || !kt->on_device || !v->on_device) return 0;
   if (kt->dims[0] != 1 || kt->dims[2] != kHD || v->dims[0] != 1 || v->dims[3] != kHD) return 0;

@@ -31,6 +31,13 @@ constexpr float kWeightSumBound = 18446744073709551616.0f;
 // starts far below kWeightSumBound.
 constexpr float kFastMaxLo = -64.0f;
 constexpr float kFastMaxHi = 32.0f;
+// The same window for f16 weights, which are subnormal below 2^-14, flush to zero below 2^-24 and
+// overflow above 65504: a row max below -4 would leave every weight of the row subnormal or zero
+// (a row of scores near -40 would sum to 0), so f16 takes the fast path only when the largest
+// weight of the first subtile lies in [2^-4, 2^15]. Keys 10 log2 units below that max are then
+// still normal, and the keys that underflow weigh at most 2^-20 of the max each.
+constexpr float kFastMaxLoF16 = -4.0f;
+constexpr float kFastMaxHiF16 = 15.0f;
 
 template <int DT>
 using store_t = std::conditional_t<DT == kF32, float, uint16_t>;

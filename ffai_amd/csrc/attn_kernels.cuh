@@ -607,10 +607,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     };
     // Common path, inside the phase: weights against the current reference max m_s, with no max
     // taken. m_s starts either at 0 (FAST: every row max of the wave's first subtile lies in
-    // [kFastMaxLo, kFastMaxHi] and Q carries the scale, so a weight is exp2 of the accumulator
-    // itself) or at the row max of the first subtile; it is raised only in `settle`, when a
-    // subtile's weights leave the range below, and the wave then leaves FAST for good. Either
-    // way the largest weight of a row is at least 2^kFastMaxLo, so nothing that matters
+    // [kFastMaxLo, kFastMaxHi] ([kFastMaxLoF16, kFastMaxHiF16] for f16 weights) and Q carries
+    // the scale, so a weight is exp2 of the accumulator itself) or at the row max of the first
+    // subtile; it is raised only in `settle`, when a subtile's weights leave the range below,
+    // and the wave then leaves FAST for good. Either way the largest weight of a row is at least
+    // 2^kFastMaxLo (bf16; 2^kFastMaxLoF16, a normal number, for f16), so nothing that matters
     // underflows. Work unit: pair k (scores 2k, 2k+1) of column block c of subtile st.
     constexpr int NPAIR = QW * 8;  // pairs per subtile
     uint32_t pw[QW][8];            // packed pairs of the subtile being exponentiated
@@ -782,13 +783,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
       // the reference max: this subtile's row max (-inf if all of it is masked), or 0 for the
       // whole wave when every such max is in the FAST window
       bool wide = false;
+      constexpr float fast_lo = MODE == kF16 ? kFastMaxLoF16 : kFastMaxLo;
+      constexpr float fast_hi = MODE == kF16 ? kFastMaxHiF16 : kFastMaxHi;
 #pragma unroll
       for (int c = 0; c < QW; ++c) {
         float mx = kNegInf;
 #pragma unroll
         for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[c][0][r], sacc[c][0][r + 1]));
         m_s[c] = partner_max(mx) * qmul;
-        wide = wide || !(m_s[c] >= kFastMaxLo && m_s[c] <= kFastMaxHi);
+        wide = wide || !(m_s[c] >= fast_lo && m_s[c] <= fast_hi);
       }
       fast = D == 64 && qmul == 1.f && __builtin_amdgcn_ballot_w64(wide) == 0;
       if (fast) {

@@ -2,6 +2,10 @@
 // projections, with their outputs laid out so that the fused attention reads them by stride,
 // replacing EncoderAttention::forward (crates/ffai-mercury/src/asr/text_decoder.rs:1059-1139).
 //
+// A call runs its windows in passes of at most kMaxRows rows (one 1500-frame window for
+// whisper, several shorter ones), each pass through the same workspace, as the reference loops
+// over batch items (text_decoder.rs:1069-1076). Below, B is the windows of one pass.
+//
 // Workspace (compute dtype T = bf16 or f16; B batch, S seq, N n_state, H heads, hd = N / H):
 //   q      (B, S, N)     = x Wq^T + bq       read by the kernel as (B, H, S, hd), strides (S N, hd, N, 1)
 //   v      (B, S, N)     = x Wv^T + bv       likewise
@@ -39,8 +43,9 @@ using ffai::api_clear_error;
 using ffai::api_fail;
 
 constexpr size_t kGemmScratch = size_t(32) << 20;  // hipBLASLt workspace ceiling
-// Rows (batch * seq) per call: one 30 s window, the reference's own granularity (it loops over
-// windows, text_decoder.rs:1069-1076); larger calls are refused until they are validated.
+// Rows (windows x seq) per pass: one 30 s window, the reference's own granularity (it loops over
+// windows, text_decoder.rs:1069-1076). A call of more windows runs several passes; a single pass
+// of more rows is refused (it has not been validated on the GPU).
 constexpr int64_t kMaxRows = 1500;
 constexpr int kMaxDevices = 64;
 
@@ -167,9 +172,20 @@ int check(const ffai_encoder_attn_desc* d) {
   if (d->n_state % d->n_head) return api_fail(FFAI_ERR_INVALID, "n_state must be a multiple of n_head");
   const int hd = d->n_state / d->n_head;
   if (hd != 64 && hd != 128) return api_fail(FFAI_ERR_INVALID, "head_dim must be 64 or 128");
-  if ((int64_t)d->batch * d->seq > kMaxRows)
-    return api_fail(FFAI_ERR_INVALID, "batch * seq above 1500 rows per call is not enabled");
+  if (d->seq > kMaxRows) return api_fail(FFAI_ERR_INVALID, "seq above 1500 frames per window is not enabled");
   return FFAI_OK;
+}
+
+// The windows of one pass: as many as fit kMaxRows rows (at least one; check() bounds seq).
+int windows_per_pass(const ffai_encoder_attn_desc* d) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(d->batch, kMaxRows / d->seq));
+}
+
+// The descriptor of a pass of `windows` windows.
+ffai_encoder_attn_desc pass_desc(const ffai_encoder_attn_desc* d, int windows) {
+  ffai_encoder_attn_desc p = *d;
+  p.batch = windows;
+  return p;
 }
 
 // `packed`: q, k and v side by side in one (B, S, 3N) buffer, K read as rows.
@@ -216,32 +232,26 @@ int ffai_encoder_attn_workspace_bytes(const ffai_encoder_attn_desc* d, size_t* b
   if (!bytes) return api_fail(FFAI_ERR_INVALID, "null bytes pointer");
   int rc = check(d);
   if (rc != FFAI_OK) return rc;
+  // every pass fits the first (largest) one's layout
+  const ffai_encoder_attn_desc p = pass_desc(d, windows_per_pass(d));
   Sizes z;
-  rc = sizes_of(d, &z);
+  rc = sizes_of(&p, &z);
   if (rc != FFAI_OK) return rc;
   *bytes = z.total;
   return FFAI_OK;
 }
 
-int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
-                          const ffai_encoder_attn_weights* w, void* out, void* workspace,
-                          size_t workspace_bytes, void* stream) {
-  api_clear_error();
-  int rc = check(d);
-  if (rc != FFAI_OK) return rc;
-  if (!x || !out || !w || !w->wo || !w->bo) return api_fail(FFAI_ERR_INVALID, "null pointer");
-  const bool packed = w->wqkv && w->bqkv;
-  if (!packed && (!w->wq || !w->bq || !w->wk_scaled || !w->wv || !w->bv))
-    return api_fail(FFAI_ERR_INVALID, "null pointer (give wq, bq, wk_scaled, wv, bv or wqkv, bqkv)");
-  Sizes z;
-  if ((rc = sizes_of(d, &z)) != FFAI_OK) return rc;
-  if (!workspace || workspace_bytes < z.total)
-    return api_fail(FFAI_ERR_WORKSPACE, "workspace smaller than ffai_encoder_attn_workspace_bytes");
-  if ((uintptr_t)workspace % 256) return api_fail(FFAI_ERR_INVALID, "workspace must be 256-byte aligned");
-  if ((rc = api_check_device()) != FFAI_OK) return rc;
-  hipblasLtHandle_t h;
-  if ((rc = handle_for_current(&h)) != FFAI_OK) return rc;
+}  // extern "C"
 
+namespace {
+
+// One pass: the windows of `d` (at most kMaxRows rows) through the workspace laid out by `z`.
+int run_pass(const ffai_encoder_attn_desc* d, const void* x, const ffai_encoder_attn_weights* w,
+             bool packed, void* out, void* workspace, const Sizes& z, hipblasLtHandle_t h,
+             void* stream) {
+  if ((int64_t)d->batch * d->seq > kMaxRows)
+    return api_fail(FFAI_ERR_INVALID, "one pass holds at most 1500 rows");
+  int rc = FFAI_OK;
   char* ws = static_cast<char*>(workspace);
   void* q = ws;
   void* kt = ws + z.q;
@@ -295,6 +305,48 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   // out: (B S, N) = merged Wo^T + bo
   g.b = merged; g.a = w->wo; g.d = out; g.bias = w->bo;
   return run_gemm(h, g, dt, scratch, z.gemm, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
+                          const ffai_encoder_attn_weights* w, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  api_clear_error();
+  int rc = check(d);
+  if (rc != FFAI_OK) return rc;
+  if (!x || !out || !w || !w->wo || !w->bo) return api_fail(FFAI_ERR_INVALID, "null pointer");
+  const bool packed = w->wqkv && w->bqkv;
+  if (!packed && (!w->wq || !w->bq || !w->wk_scaled || !w->wv || !w->bv))
+    return api_fail(FFAI_ERR_INVALID, "null pointer (give wq, bq, wk_scaled, wv, bv or wqkv, bqkv)");
+  const int wpp = windows_per_pass(d);
+  const ffai_encoder_attn_desc first = pass_desc(d, wpp);
+  Sizes z;
+  if ((rc = sizes_of(&first, &z)) != FFAI_OK) return rc;
+  if (!workspace || workspace_bytes < z.total)
+    return api_fail(FFAI_ERR_WORKSPACE, "workspace smaller than ffai_encoder_attn_workspace_bytes");
+  if ((uintptr_t)workspace % 256) return api_fail(FFAI_ERR_INVALID, "workspace must be 256-byte aligned");
+  if ((rc = api_check_device()) != FFAI_OK) return rc;
+  hipblasLtHandle_t h;
+  if ((rc = handle_for_current(&h)) != FFAI_OK) return rc;
+  // passes in window order, stream-ordered through the one workspace (the reference's loop over
+  // batch items); a last, shorter pass lays its buffers out within the first pass's regions
+  const size_t window_bytes = (size_t)d->seq * d->n_state * 2;
+  for (int b0 = 0; b0 < d->batch; b0 += wpp) {
+    const ffai_encoder_attn_desc p = pass_desc(d, std::min(wpp, d->batch - b0));
+    Sizes zp;
+    if ((rc = sizes_of(&p, &zp)) != FFAI_OK) return rc;
+    // the pass's regions keep the first pass's offsets (each region of a shorter pass is no
+    // larger than the first pass's)
+    zp.q = z.q; zp.kt = z.kt; zp.v = z.v; zp.merged = z.merged; zp.gemm = z.gemm;
+    zp.attn = z.attn;
+    rc = run_pass(&p, static_cast<const char*>(x) + b0 * window_bytes, w, packed,
+                  static_cast<char*>(out) + b0 * window_bytes, workspace, zp, h, stream);
+    if (rc != FFAI_OK) return rc;
+  }
+  return FFAI_OK;
 }
 
 }  // extern "C"

@@ -93,7 +93,9 @@ struct AppendParams {
 template <int SRC, int DST>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int s = blockIdx.x;
-  const int len0 = p.lens[s];
+  // a length outside [0, capacity] (corrupt or uninitialised) is clamped, as the gather does, so
+  // no row lands before the slot's cache or past it
+  const int len0 = min(max(p.lens[s], 0), p.capacity);
   const int row_units = p.heads * p.head_dim / 8;
   const int units = p.t_new * row_units;
   const int u_begin = blockIdx.y * p.units_per_block;
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
 __global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* lens, int slots, int capacity,
                                                          int t_new) {
   const int s = blockIdx.x * 256 + threadIdx.x;
-  if (s < slots) lens[s] = min(capacity, lens[s] + t_new);
+  if (s < slots) lens[s] = min(capacity, min(max(lens[s], 0), capacity) + t_new);
 }
 
 struct GatherParams {

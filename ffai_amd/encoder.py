@@ -3,7 +3,8 @@
 Mirrors EncoderAttention (crates/ffai-mercury/src/asr/text_decoder.rs:1009-1139): `load` folds
 head_dim^-0.5 into the key weight once (:1039-1050); `forward` runs the q / k^T / v projections,
 the fused attention and the out-projection in one stream-ordered library call (hipBLASLt GEMMs
-around ffai_attn_fwd), with no head-split copies and the whole batch at once.
+around ffai_attn_fwd), with no head-split copies. Inside the call the windows run in passes of at
+most 1500 rows through one workspace, as the reference loops over batch items (:1069-1076).
 """
 
 from __future__ import annotations

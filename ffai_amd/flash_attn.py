@@ -203,6 +203,16 @@ def workspace_bytes(q, k, v, out, **kw) -> int:
     return n.value
 
 
+def plan(q, k, v, out, **kw) -> dict:
+    """The launch plan ffai_attn_fwd uses for these operands (ffai_attn_plan_info), assuming
+    the kernels' vector alignment: kernel, workgroup shape, key splits, tiles per split and
+    workgroups."""
+    desc = make_desc(q, k, v, out, k_transposed=kw.get("k_transposed", False),
+                     scale=kw.get("scale", 1.0), causal=kw.get("causal", False),
+                     q_offset=kw.get("q_offset", 0), kv_lens=kw.get("kv_lens"))
+    return L.plan_info(desc)
+
+
 def serves_desc(q_dtype: torch.dtype, kv_dtype: torch.dtype, out_dtype: torch.dtype,
                 shape: Sequence[int], *, k_transposed: bool = False, causal: bool = False) -> bool:
     """ffai_attn_serves for packed operands: shape = (batch, heads_q, heads_kv, q_len, kv_len,

@@ -101,6 +101,16 @@ int ffai_attn_workspace_bytes(const ffai_attn_desc* d, size_t* bytes);
 int ffai_attn_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v,
                   void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Diagnostic, no counterpart in the reference: the launch plan ffai_attn_fwd uses for `d` when
+ * every operand admits the kernels' vector accesses (16-byte aligned bases and strides), so a
+ * test or benchmark can state which kernel shape it ran. info[0]: kernel (0 the fused
+ * encoder/prefill kernel, 1 the decode kernel); info[1]: workgroup shape (fused: 0 one wave x
+ * 32 query rows, 1 four waves x 32 rows, 2 four waves x 64 rows; decode: waves per workgroup);
+ * info[2]: key splits per work item (1 = no partials); info[3]: 64-key tiles per split;
+ * info[4]: workgroups. Returns FFAI_OK, FFAI_DECLINED or FFAI_ERR_INVALID as
+ * ffai_attn_workspace_bytes. */
+int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]);
+
 /* ------------------------------------------------------------------------------------------
  * Mirrors of the reference's public functions.
  * ---------------------------------------------------------------------------------------- */

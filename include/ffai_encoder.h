@@ -10,9 +10,11 @@
  *   out = merged Wo^T + bo                (self.inner.out, :1126)
  * The reference splits q and v into heads with a copy each (:1103-1117) and loops over batch
  * items (:1069-1076). Here the projections land in the layouts the kernel reads by stride (no
- * copies) and the batch is one launch per GEMM: hipBLASLt GEMMs with bias epilogues (bf16/f16
- * in and out, f32 accumulation) around ffai_attn_fwd. With packed weights (wqkv, bqkv) the
- * three input projections are one GEMM.
+ * copies): hipBLASLt GEMMs with bias epilogues (bf16/f16 in and out, f32 accumulation) around
+ * ffai_attn_fwd. With packed weights (wqkv, bqkv) the three input projections are one GEMM. The
+ * windows run in passes of at most 1500 rows (one 30 s window, or several shorter ones per
+ * pass), each pass one launch per GEMM and one attention call, all through the same workspace;
+ * a window of more than 1500 frames is refused.
  *
  * All calls are asynchronous on `stream` (a hipStream_t; NULL = null stream), allocate nothing,
  * take device pointers and return FFAI_OK or a negative ffai_status (ffai_attn.h), with the
@@ -59,8 +61,8 @@ typedef struct ffai_encoder_attn_weights {
 } ffai_encoder_attn_weights;
 
 /* Bytes of device workspace ffai_encoder_attn_fwd needs for `d`, packed weights or not: q, k and
- * v and the merged attention output in the compute dtype, the attention's own workspace, and
- * GEMM scratch. */
+ * v and the merged attention output of one pass (at most 1500 rows) in the compute dtype, the
+ * attention's own workspace, and GEMM scratch. */
 int ffai_encoder_attn_workspace_bytes(const ffai_encoder_attn_desc* d, size_t* bytes);
 
 /* x: (batch, seq, n_state) row-major; out: the same shape. workspace: at least

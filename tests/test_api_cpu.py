@@ -106,6 +106,20 @@ def test_fwd_declines_and_rejects_without_touching_the_gpu(lib):
     assert lib.ffai_attn_fwd(ctypes.byref(d), None, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_ERR_INVALID
 
 
+@pytest.mark.parametrize("bad", [float("nan"), -float("nan"), float("inf"), -float("inf"), 0.0,
+                                 -0.0])
+def test_non_finite_or_non_positive_scale_is_an_error(lib, bad):
+    """The descriptor check rejects a NaN, infinite or non-positive scale before any launch (the
+    host code is built with IEEE NaN semantics; only device code assumes no NaNs)."""
+    d = desc(lib, L.BF16, L.BF16, L.BF16, 1, 6, 6, 100, 100, 64)
+    d.scale = bad
+    assert lib.ffai_attn_serves(ctypes.byref(d)) == 0
+    assert lib.ffai_attn_fwd(ctypes.byref(d), FAKE, FAKE, FAKE, FAKE, None, 0, None) == L.FFAI_ERR_INVALID
+    assert "scale" in L.last_error()
+    n = ctypes.c_size_t(0)
+    assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == L.FFAI_ERR_INVALID
+
+
 def test_workspace_only_for_split_shapes(lib):
     n = ctypes.c_size_t(0)
     big = desc(lib, L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED)
@@ -280,9 +294,21 @@ def test_encoder_attn_rejects_bad_arguments(lib):
     act = 1500 * 1280 * 2
     assert n.value >= 4 * act  # q, k^T, v and the merged output at least
     for bad in (desc(dtype=L.F32), desc(n_head=7), desc(n_state=640, n_head=20), desc(seq=0),
-                desc(batch=16)):  # more than one 1500-frame window of rows per call
+                desc(seq=1501)):  # one window of more than 1500 frames: a pass above 1500 rows
         assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(bad), ctypes.byref(n)) == \
             L.FFAI_ERR_INVALID
+    # the large-v3 batch of 16 windows runs as 16 passes of one window through one window's
+    # workspace; 5 windows of 300 frames fit one pass
+    one = ctypes.c_size_t(0)
+    assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(desc()), ctypes.byref(one)) == L.FFAI_OK
+    assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(desc(batch=16)), ctypes.byref(n)) == L.FFAI_OK
+    assert n.value == one.value
+    five = ctypes.c_size_t(0)
+    assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(desc(batch=5, seq=300)),
+                                                 ctypes.byref(five)) == L.FFAI_OK
+    assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(desc(batch=11, seq=300)),
+                                                 ctypes.byref(n)) == L.FFAI_OK
+    assert n.value == five.value
     w = L.EncoderAttnWeights()  # all null
     assert lib.ffai_encoder_attn_fwd(ctypes.byref(desc()), FAKE, ctypes.byref(w), FAKE, FAKE,
                                      1 << 40, None) == L.FFAI_ERR_INVALID

@@ -77,3 +77,31 @@ def test_encoder_block_batch_equals_items(gpu):
         one = ea(dev(x[i:i + 1]))
         err = (allx[i:i + 1].float() - one.float()).abs().max().item()
         assert err <= 2e-2, (i, err)
+
+
+def test_encoder_block_windows_run_in_passes(gpu):
+    """Eleven 300-frame windows (whisper-tiny width) run as passes of five, five and one window
+    (at most 1500 rows per pass) through one workspace sized for a pass; every window matches
+    the oracle."""
+    rng = np.random.default_rng(63)
+    x, ws = _case(rng, 11, 300, 384, "bf16")
+    for packed in (True, False):
+        got, want = _run(gpu, x, ws, 6, "bf16", packed)
+        err = max_abs(got, want)
+        print(f"encoder block 11 x 300 packed={packed}: {err:.3e}")
+        assert err < TOL_BF16
+
+
+def test_encoder_block_full_windows_equal_single_calls(gpu):
+    """Three 1500-frame windows at whisper-large-v3 width run as three one-window passes: each
+    window's output equals a one-window call bit for bit (the same GEMM and attention shapes on
+    the same data), and the workspace is one window's."""
+    rng = np.random.default_rng(64)
+    x, ws = _case(rng, 3, 1500, 1280, "bf16")
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu, torch.bfloat16)
+    ea = EncoderAttention.load(1280, 20, *[dev(w) for w in ws])
+    assert ea.workspace_bytes(dev(x)) == ea.workspace_bytes(dev(x[:1]))
+    allx = ea(dev(x))
+    for i in range(3):
+        one = ea(dev(x[i:i + 1]))
+        assert torch.equal(allx[i:i + 1], one), i

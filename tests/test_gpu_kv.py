@@ -59,6 +59,33 @@ def test_append_matches_concatenation(gpu, src, dst):
         np.testing.assert_array_equal(v[s, :, :n], want_v)
 
 
+@pytest.mark.parametrize("t_new", [1, 200])
+def test_append_clamps_lengths_out_of_range(gpu, t_new):
+    """A corrupt length (negative, or above capacity) is clamped into [0, capacity] before the
+    append, as the gather clamps it: rows of a slot at -1 land from position 0, a slot past
+    capacity takes nothing, and no row lands outside the slot's cache. One row (one workgroup
+    per slot, length advanced in the same launch) and 200 rows (several workgroups per slot,
+    separate length update)."""
+    rng = np.random.default_rng(17)
+    slots, heads, d, cap = 3, 4, 64, 256
+    cache = KVCache(slots, heads, cap, d, torch.bfloat16, gpu)
+    old_k = okv.round_to(randn(rng, cache.k.shape), "bf16")
+    cache.k.copy_(torch.from_numpy(old_k))
+    start = np.array([-1, -1000, cap + 7], np.int32)
+    cache.lens.copy_(torch.from_numpy(start))
+    nk = randn(rng, (slots, t_new, heads * d))
+    nv = randn(rng, (slots, t_new, heads * d))
+    cache.append(_dev(nk, torch.float32, gpu), _dev(nv, torch.float32, gpu))
+    lens = cache.lens.cpu().numpy()
+    np.testing.assert_array_equal(lens, [min(t_new, cap), min(t_new, cap), cap])
+    k = cache.k.float().cpu().numpy()
+    for s in (0, 1):
+        want = okv.round_to(okv.split_heads(nk[s:s + 1], heads)[0], "bf16")
+        np.testing.assert_array_equal(k[s, :, :t_new], want)
+        np.testing.assert_array_equal(k[s, :, t_new:], old_k[s, :, t_new:])
+    np.testing.assert_array_equal(k[2], old_k[2])  # a slot past capacity is untouched
+
+
 def test_long_append_spans_workgroups(gpu):
     """A 200-row append (a prompt's size: 25600 8-element units per slot, several workgroups per
     slot and a separate length update) into ragged slots, one of which runs past capacity."""

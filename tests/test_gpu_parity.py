@@ -177,6 +177,48 @@ def test_first_subtile_outside_the_fast_window(gpu, dtype, sign):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("row_max", [-40.0, -20.0])
+@pytest.mark.parametrize("shape", [(2, 64, 300), (1, 2, 300), (1, 16, 200)])
+def test_scores_shifted_far_below_zero(gpu, dtype, row_max, shape):
+    """Softmax ignores a shift shared by every score of a row. Q's dimension 0 is set to c and
+    K's dimension 0 to -1 for every key, which moves every score of every row by -c * scale;
+    c puts the row maxima near `row_max` log2 units, where exp2 of a raw score is below f16's
+    normal range (2^-14) or flushes to 0 (2^-24). The output must still equal the oracle on the
+    unshifted inputs (dimension 0 zero in both), in both 16-bit types and in the three launch
+    shapes: four waves x 64 rows (2 x 64 heads), four waves x 32 rows with split keys, one wave
+    x 32 rows (200 rows)."""
+    rng = np.random.default_rng(33)
+    b, h, t = shape
+    d = 64
+    rnd = round_bf16 if dtype == torch.bfloat16 else round_f16
+    scale = 0.125
+    q = rnd(randn(rng, (b, h, t, d)))
+    k = rnd(randn(rng, (b, h, t, d)))
+    v = rnd(randn(rng, (b, h, t, d)))
+    q[..., 0] = 0.0
+    k[..., 0] = 0.0
+    # unshifted row maxima are a few log2 units above 0: shift them to about row_max
+    c = np.float32((3.0 - row_max) / (scale * np.log2(np.e)))
+    qs, ks = q.copy(), k.copy()
+    qs[..., 0] = rnd(np.full(q.shape[:3], c, np.float32))
+    ks[..., 0] = -1.0
+    shifted = textbook.attention(qs, ks, v, scale=scale, rows=np.arange(32))
+    unshifted = textbook.attention(q, k, v, scale=scale, rows=np.arange(32))
+    assert max_abs(shifted, unshifted) < 1e-9  # the identity itself, in float64
+    s_max = (np.einsum("bhtd,bhsd->bhts", qs[:, :, :32], ks[:, :, :32]).max(-1) * scale *
+             np.log2(np.e))
+    assert np.all(s_max < row_max + 6) and np.all(s_max > row_max - 6), (s_max.min(), s_max.max())
+    out = fa.attention(_dev(qs, dtype, gpu), _dev(ks, dtype, gpu), _dev(v, dtype, gpu),
+                       scale=scale, out_dtype=torch.float32)
+    got = _host(out)
+    assert np.isfinite(got).all()
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=scale)
+    err = max_abs(got, want)
+    print(f"shifted scores {dtype} row max ~{row_max} shape {shape}: {err:.3e}")
+    assert err < TOL_BF16
+
+
 @pytest.mark.parametrize("k_transposed", [True, False])
 def test_f16_query_beyond_the_folding_range(gpu, k_transposed):
     """The 16-bit kernel folds scale * log2(e) into Q. With scale 1, f16 query elements above
