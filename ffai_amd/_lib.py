@@ -108,6 +108,8 @@ def load():
     L.ffai_attn_workspace_bytes.argtypes = [dp, ctypes.POINTER(sz)]
     L.ffai_attn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     L.ffai_attn_plan_info.argtypes = [dp, ctypes.POINTER(ctypes.c_int32)]
+    L.ffai_attn_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp]
+    L.ffai_attn_noalloc_scratch_bytes.restype = sz
     L.ffai_serves.argtypes = [tp, tp]
     L.ffai_attend.argtypes = [tp, tp, tp, ctypes.c_int, tp, vp, sz, vp]
     L.ffai_attend_workspace_bytes.argtypes = [tp, tp, tp, ctypes.POINTER(sz)]
@@ -131,7 +133,7 @@ def load():
     L.ffai_vocab_int8_logits.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, i64, vp,
                                          ctypes.c_size_t, vp]
     for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd",
-                 "ffai_attn_plan_info", "ffai_serves",
+                 "ffai_attn_plan_info", "ffai_attn_fwd_noalloc", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
                  "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",

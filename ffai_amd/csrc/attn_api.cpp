@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "attn_kernels.h"
@@ -246,8 +247,39 @@ size_t plan_ws_bytes(const ffai_attn_desc* d) {
   return std::max(make_plan(d, true, true).ws_bytes, make_plan(d, true, false).ws_bytes);
 }
 
+// ---- allocation-free entry point: a library-owned split-key scratch per device ----------------
+// ffai_attn_fwd_noalloc keeps the split-key partials in this array instead of a caller
+// workspace. Every plan of ffai_attn_fwd needs at most ~51 MB of partials (head_dim 128,
+// 16-bit, three splits of a grid under 256 workgroups); a plan above kScratchBytes is refused.
+// In host code `scratch` names a host-side stand-in, not device memory: the device address is
+// taken once per device with hipGetSymbolAddress (that device current) and kept in
+// g_scratch_ptr; only that address is handed to kernels. The array lives until the process
+// ends, and every call on one device shares it.
+constexpr size_t kScratchBytes = size_t(48) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch (hipGetSymbolAddress on first use per device).
+int scratch_for_current(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FFAI_ERR_HIP, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FFAI_ERR_DEVICE, "device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FFAI_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return FFAI_OK;
+}
+
+// `use_scratch`: the partials go to the library's scratch (ws and ws_bytes are ignored).
 int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v, void* out,
-            void* ws, size_t ws_bytes, void* stream, bool allow_split) {
+            void* ws, size_t ws_bytes, void* stream, bool allow_split, bool use_scratch = false) {
   g_last_error.clear();
   std::string why;
   const int rc = check_desc(d, &why);
@@ -257,8 +289,6 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   const size_t qs = elem_size(d->q_dtype), ks = elem_size(d->kv_dtype), os = elem_size(d->out_dtype);
   if ((uintptr_t)q % qs || (uintptr_t)k % ks || (uintptr_t)v % ks || (uintptr_t)out % os)
     return fail(FFAI_ERR_INVALID, "operand pointer not aligned to its element size");
-  const int dev = check_device();
-  if (dev != FFAI_OK) return dev;
 
   const bool f32 = d->q_dtype == FFAI_F32;
   const bool kt = d->k_layout == FFAI_K_TRANSPOSED;
@@ -271,6 +301,18 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
                        vec_of(out, os, d->o_strides, 4) == 4;
 
   const Plan pl = make_plan(d, allow_split, aligned);
+  if (use_scratch && pl.ws_bytes > kScratchBytes)
+    return fail(FFAI_ERR_WORKSPACE,
+                "this shape needs " + std::to_string(pl.ws_bytes) +
+                    " bytes of split-key partials; the allocation-free entry point holds at most " +
+                    std::to_string(kScratchBytes) + " (use ffai_attn_fwd with a workspace)");
+  const int dev = check_device();
+  if (dev != FFAI_OK) return dev;
+  if (use_scratch && pl.ws_bytes > 0) {
+    const int src = scratch_for_current(&ws);
+    if (src != FFAI_OK) return src;
+    ws_bytes = kScratchBytes;
+  }
   if (pl.ws_bytes > 0) {
     if (!ws || ws_bytes < pl.ws_bytes)
       return fail(FFAI_ERR_WORKSPACE, "workspace smaller than ffai_attn_workspace_bytes");
@@ -458,6 +500,13 @@ int ffai_attn_fwd(const ffai_attn_desc* d, const void* q, const void* k, const v
                   void* out, void* workspace, size_t workspace_bytes, void* stream) {
   return run_fwd(d, q, k, v, out, workspace, workspace_bytes, stream, true);
 }
+
+int ffai_attn_fwd_noalloc(const ffai_attn_desc* d, const void* q, const void* k, const void* v,
+                          void* out, void* stream) {
+  return run_fwd(d, q, k, v, out, nullptr, 0, stream, true, true);
+}
+
+size_t ffai_attn_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]) {
   if (!info) return fail(FFAI_ERR_INVALID, "null info pointer");

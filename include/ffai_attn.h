@@ -101,6 +101,22 @@ int ffai_attn_workspace_bytes(const ffai_attn_desc* d, size_t* bytes);
 int ffai_attn_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v,
                   void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): ffai_attn_fwd
+ * without a workspace argument. The split-key partials go to a scratch array the library owns,
+ * one per device (ffai_attn_noalloc_scratch_bytes(): 48 MiB, held from the first call on a
+ * device until the process ends); the call allocates nothing and otherwise runs exactly
+ * ffai_attn_fwd's plan and kernels, so its output is the same. A shape whose partials exceed
+ * the scratch returns FFAI_ERR_WORKSPACE. Every call on one device shares that device's
+ * scratch: calls that may overlap on one device (different streams, unordered) race; calls
+ * ordered on one stream, and replays of captured graphs, do not. The scratch keeps the last
+ * call's partials; nothing in it needs clearing between calls. */
+int ffai_attn_fwd_noalloc(const ffai_attn_desc* d, const void* q, const void* k, const void* v,
+                          void* out, void* stream);
+
+/* Size in bytes of the per-device scratch behind ffai_attn_fwd_noalloc. */
+size_t ffai_attn_noalloc_scratch_bytes(void);
+
 /* Diagnostic, no counterpart in the reference: the launch plan ffai_attn_fwd uses for `d` when
  * every operand admits the kernels' vector accesses (16-byte aligned bases and strides), so a
  * test or benchmark can state which kernel shape it ran. info[0]: kernel (0 the fused
