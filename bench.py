@@ -86,7 +86,7 @@ def encoder_bench(torch, fa, steps, warmup, layers, B=16, H=20, T=1500, D=64,
     ws = None
     nbytes = fa.workspace_bytes(*bufs[0], k_transposed=kt_layout, scale=scale, causal=causal)
     if nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
 
     def step():
         for q, k, v, o in bufs:
@@ -177,9 +177,9 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
         all_sets.append(layer_bufs)
     # workspaces (one per call site, reused across layers: calls are stream-ordered)
     qs, ks, vs, ls, os_, qx, ktx, vx, ox = all_sets[0][0]
-    ws_self = torch.empty(max(1, fa.workspace_bytes(qs, ks, vs, os_, scale=scale, kv_lens=ls)),
+    ws_self = torch.zeros(max(1, fa.workspace_bytes(qs, ks, vs, os_, scale=scale, kv_lens=ls)),
                           dtype=torch.uint8, device=dev)
-    ws_x = torch.empty(max(1, fa.workspace_bytes(qx.permute(2, 1, 0, 3), ktx, vx,
+    ws_x = torch.zeros(max(1, fa.workspace_bytes(qx.permute(2, 1, 0, 3), ktx, vx,
                                                  ox.permute(2, 1, 0, 3), k_transposed=True,
                                                  scale=scale)), dtype=torch.uint8, device=dev)
 
@@ -276,9 +276,9 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
     o_self = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
     o_x = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
     q0, k0 = projs[0][2], caches[0].layer(0)
-    ws_self = torch.empty(max(1, fa.workspace_bytes(q0, k0.k, k0.v, o_self, scale=scale,
+    ws_self = torch.zeros(max(1, fa.workspace_bytes(q0, k0.k, k0.v, o_self, scale=scale,
                                                     kv_lens=k0.lens)), dtype=torch.uint8, device=dev)
-    ws_x = torch.empty(max(1, fa.workspace_bytes(projs[0][3].permute(2, 1, 0, 3), xs[0][2][None],
+    ws_x = torch.zeros(max(1, fa.workspace_bytes(projs[0][3].permute(2, 1, 0, 3), xs[0][2][None],
                                                  xs[0][3][None], o_x.permute(2, 1, 0, 3),
                                                  k_transposed=True, scale=scale)),
                        dtype=torch.uint8, device=dev)
@@ -358,7 +358,7 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
     pv = torch.randn(1, P, H * D, generator=gd, device=dev)
     pq = torch.randn(1, H, P, D, generator=gd, device=dev).to(bf)
     po = torch.empty(1, H, P, D, device=dev, dtype=torch.float32)
-    pws = torch.empty(max(1, fa.workspace_bytes(pq, xs[0][2][None], xs[0][3][None], po,
+    pws = torch.zeros(max(1, fa.workspace_bytes(pq, xs[0][2][None], xs[0][3][None], po,
                                                 k_transposed=True, scale=scale)),
                       dtype=torch.uint8, device=dev)
 
@@ -421,7 +421,7 @@ def encoder_block_bench(torch, fa, steps, warmup, layers=4, windows=16, T=1500, 
         ea = EncoderAttention.load(n, H, w[0], bias[0], w[1], w[2], bias[1], w[3], bias[2])
         xs = [torch.randn(1, T, n, generator=g, device=dev).to(bf) for _ in range(windows)]
         blocks.append((ea, xs, [torch.empty_like(x) for x in xs]))
-    ws = torch.empty(blocks[0][0].workspace_bytes(blocks[0][1][0]), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(blocks[0][0].workspace_bytes(blocks[0][1][0]), dtype=torch.uint8, device=dev)
 
     def step():
         for ea, xs, outs in blocks:

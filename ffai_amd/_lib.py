@@ -118,6 +118,9 @@ def load():
     L.ffai_get_decode_min_keys.restype = ctypes.c_int
     L.ffai_set_decode_min_keys.argtypes = [ctypes.c_int]
     L.ffai_set_decode_min_keys.restype = None
+    L.ffai_get_decode_tiles_per_wg.restype = ctypes.c_int
+    L.ffai_set_decode_tiles_per_wg.argtypes = [ctypes.c_int]
+    L.ffai_set_decode_tiles_per_wg.restype = None
     L.ffai_attn_last_error.restype = ctypes.c_char_p
     cp = ctypes.POINTER(KVCacheView)
     i32, i64 = ctypes.c_int32, ctypes.c_int64

@@ -65,6 +65,26 @@ int decode_min_keys() {
   return v;
 }
 
+// Tuning knob, no counterpart in the reference: 64-key tiles per decode workgroup (0 = the
+// planner's choice). Initialised from FFAI_DECODE_TILES_PER_WG on first use.
+std::atomic<int> g_decode_tps{-1};
+
+int decode_tiles_per_wg() {
+  int v = g_decode_tps.load(std::memory_order_relaxed);
+  if (v < 0) {
+    int init = 0;
+    if (const char* e = std::getenv("FFAI_DECODE_TILES_PER_WG")) {
+      char* end = nullptr;
+      const long n = std::strtol(e, &end, 10);
+      if (end != e && *end == '\0' && n > 0 && n < (1L << 20)) init = (int)n;
+    }
+    int expected = -1;
+    g_decode_tps.compare_exchange_strong(expected, init, std::memory_order_relaxed);
+    v = g_decode_tps.load(std::memory_order_relaxed);
+  }
+  return v;
+}
+
 constexpr int kMinSeq = 256;  // flash_attn.rs:55 (MIN_SEQ)
 constexpr int kHD = 64;       // flash_attn.rs:50
 
@@ -137,10 +157,11 @@ struct Plan {
 };
 
 // Decode launch: 16-bit inputs and at most 32 query rows per (batch, kv-head), so one MFMA
-// column block holds every row that reads a K/V head. A workgroup of 8 waves (4 at head_dim
-// 128, for LDS) gives one 64-key tile to each wave; a unit with more tiles than that is split
-// over workgroups whose partials decode_combine_kernel merges. When the units alone leave the
-// GPU short of workgroups, a workgroup takes fewer tiles so that more of them stream keys.
+// column block holds every row that reads a K/V head. Each wave of a workgroup takes one 64-key
+// tile. A unit with more tiles than its workgroup's waves is split over workgroups, whose
+// partials the unit's last workgroup merges in the same launch (counters at the workspace's
+// start). When the units alone leave the GPU short of workgroups, a workgroup takes fewer tiles
+// so that more of them stream keys at once.
 bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
   const int group = d->heads_q / d->heads_kv;
   const int64_t rows = (int64_t)group * d->q_len;
@@ -150,35 +171,40 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
   int64_t kv_blk = d->kv_len;
   if (d->causal) kv_blk = std::min<int64_t>(kv_blk, (int64_t)d->q_offset + d->q_len);
   const int64_t n_tiles = std::max<int64_t>(1, (kv_blk + ffai::kBlockN - 1) / ffai::kBlockN);
-  const int waves = d->head_dim == 64 ? 8 : 4;
-  // Splitting costs a combine launch (~3 us), so a grid of at least kMinWorkgroups stays whole;
-  // a smaller one is split towards kSplitWorkgroups (whisper-medium cross-attention, 16 heads x
-  // 24 tiles: 10.0 us per layer at 128 workgroups, 10.9 at 64, 15.5 unsplit; the beam-5
-  // self-attention's 80 unsplit workgroups, 7.7 us, against 10.1 split in two).
+  const int max_waves = d->head_dim == 64 ? 8 : 4;  // LDS: 16 KB (32 KB at head_dim 128) a wave
+  // A grid of at least kMinWorkgroups stays at max_waves tiles per workgroup; a smaller one is
+  // split towards kSplitWorkgroups. A split costs the unit's last workgroup ~3.5 us of device-
+  // scope round trips (its partial acknowledged, the counter, the other partials), about what a
+  // second launch cost. Measured, beam-5 whisper-medium step (24 layers, graphs), tiles per
+  // workgroup for the cross-attention (16 heads x 24 tiles): 1: 397 us, 2: 249, 3: 224, 4: 225,
+  // 6: 241, 8: 253, 24 (unsplit): 375; the self-attention's 80 units split at all: 191-212
+  // against 165 unsplit.
   constexpr int64_t kMinWorkgroups = 64, kSplitWorkgroups = 128;
-  int64_t tps = waves;
+  int64_t tps = max_waves;
   if (units * ((n_tiles + tps - 1) / tps) < kMinWorkgroups)
     tps = std::max<int64_t>(1, n_tiles * units / kSplitWorkgroups);
-  // FFAI_DECODE_TILES_PER_WG (> 0) forces the 64-key tiles per decode workgroup: a tuning knob.
-  static const int forced_tps = [] {
-    const char* e = std::getenv("FFAI_DECODE_TILES_PER_WG");
-    return e ? std::atoi(e) : 0;
-  }();
+  // a tuning knob (ffai_set_decode_tiles_per_wg / FFAI_DECODE_TILES_PER_WG) may force it
+  const int forced_tps = decode_tiles_per_wg();
   if (forced_tps > 0) tps = forced_tps;
   tps = std::min(tps, n_tiles);
-  // the combine stages all of a unit's partials in LDS
-  const int64_t max_splits = std::max<int64_t>(1, ffai::kCombineLdsFloats / (rows * (d->head_dim + 2)));
-  if ((n_tiles + tps - 1) / tps > max_splits) tps = (n_tiles + max_splits - 1) / max_splits;
+  // splits need a counter slot per unit and stay within the merge's bound
+  if (units > ffai::kCounterSlots) tps = n_tiles;
+  if ((n_tiles + tps - 1) / tps > ffai::kMaxDecodeSplits)
+    tps = (n_tiles + ffai::kMaxDecodeSplits - 1) / ffai::kMaxDecodeSplits;
   p->decode = true;
-  // a split of at most four tiles runs on four waves: half the merge through LDS (beam-5
-  // whisper-medium step: 442 -> 438 us)
-  p->waves = (d->head_dim == 64 && tps <= 4) ? 4 : waves;
+  // as many waves as tiles per workgroup (1, 2, 4 or max_waves); a workgroup's waves loop when
+  // it holds more tiles than that
+  int waves = 1;
+  while (waves < tps && waves < max_waves) waves *= 2;
+  p->waves = waves;
   p->variant = 0;
   p->n_qblk = 1;
   p->tiles_per_split = (int)tps;
   p->n_split = (int)((n_tiles + tps - 1) / tps);
   p->n_work = (int)(units * p->n_split);
-  p->ws_bytes = p->n_split > 1 ? (size_t)units * p->n_split * rows * (d->head_dim + 2) * 4 : 0;
+  p->ws_bytes = p->n_split > 1
+                    ? ffai::kCounterBytes + (size_t)units * p->n_split * rows * (d->head_dim + 2) * 4
+                    : 0;
   return true;
 }
 
@@ -238,7 +264,9 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok) {
     p.n_split = (n_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
   }
   p.n_work = (int)(work * p.n_split);
-  p.ws_bytes = p.n_split > 1 ? (size_t)bh * p.n_split * d->q_len * (d->head_dim + 2) * 4 : 0;
+  p.ws_bytes = p.n_split > 1 ? ffai::kCounterBytes +
+                                   (size_t)bh * p.n_split * d->q_len * (d->head_dim + 2) * 4
+                             : 0;
   return p;
 }
 
@@ -248,9 +276,11 @@ size_t plan_ws_bytes(const ffai_attn_desc* d) {
 }
 
 // ---- allocation-free entry point: a library-owned split-key scratch per device ----------------
-// ffai_attn_fwd_noalloc keeps the split-key partials in this array instead of a caller
-// workspace. Every plan of ffai_attn_fwd needs at most ~51 MB of partials (head_dim 128,
-// 16-bit, three splits of a grid under 256 workgroups); a plan above kScratchBytes is refused.
+// ffai_attn_fwd_noalloc keeps the split counters and split-key partials in this array instead
+// of a caller workspace (the counters start at zero, as a static array does, and every call
+// leaves them zero). Every plan of ffai_attn_fwd needs at most ~51 MB of workspace (head_dim
+// 128, 16-bit, three splits of a grid under 256 workgroups); a plan above kScratchBytes is
+// refused.
 // In host code `scratch` names a host-side stand-in, not device memory: the device address is
 // taken once per device with hipGetSymbolAddress (that device current) and kept in
 // g_scratch_ptr; only that address is handed to kernels. The array lives until the process
@@ -323,10 +353,15 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   const int kvt = d->kv_dtype == FFAI_F32 ? ffai::kF32 : (d->kv_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
   const int ot = d->out_dtype == FFAI_F32 ? ffai::kF32 : (d->out_dtype == FFAI_BF16 ? ffai::kBF16 : ffai::kF16);
 
+  // workspace: split counters first (decode plans), then the partials
+  float* partials = pl.ws_bytes > 0
+                        ? reinterpret_cast<float*>(static_cast<char*>(ws) + ffai::kCounterBytes)
+                        : nullptr;
   if (pl.decode) {
     ffai::DecodeParams p{};
     p.q = q; p.k = k; p.v = v; p.o = out;
-    p.ws = static_cast<float*>(ws);
+    p.ws = partials;
+    p.counters = static_cast<int32_t*>(ws);
     p.kv_lens = d->kv_lens;
     p.q_sb = d->q_strides[0]; p.q_sh = d->q_strides[1]; p.q_st = d->q_strides[2];
     p.k_sb = d->k_strides[0]; p.k_sh = d->k_strides[1]; p.k_st = d->k_strides[2];
@@ -344,7 +379,7 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
 
   ffai::FwdParams p{};
   p.q = q; p.k = k; p.v = v; p.o = out;
-  p.ws = static_cast<float*>(ws);
+  p.ws = partials;
   p.kv_lens = d->kv_lens;
   p.q_sb = d->q_strides[0]; p.q_sh = d->q_strides[1]; p.q_st = d->q_strides[2];
   p.k_sb = d->k_strides[0]; p.k_sh = d->k_strides[1]; p.k_st = d->k_strides[2];
@@ -597,6 +632,12 @@ int ffai_attend_merged_workspace_bytes(const ffai_tensor* q, const ffai_tensor* 
 }
 
 int ffai_get_decode_min_keys(void) { return decode_min_keys(); }
+
+int ffai_get_decode_tiles_per_wg(void) { return decode_tiles_per_wg(); }
+
+void ffai_set_decode_tiles_per_wg(int n) {
+  if (n >= 0) g_decode_tps.store(n, std::memory_order_relaxed);
+}
 
 void ffai_set_decode_min_keys(int n) {
   if (n >= 0) g_decode_min_keys.store(n, std::memory_order_relaxed);

@@ -41,6 +41,7 @@ struct DecodeParams {
   const void* v;
   void* o;
   float* ws;              // split partials: [B*Hkv][n_split][R][D] O, then [..][R][2] (m, l)
+  int32_t* counters;      // split counters, one per unit: zero before the launch, zero after
   const int32_t* kv_lens; // device int32[B] or nullptr
   int64_t q_sb, q_sh, q_st;
   int64_t k_sb, k_sh, k_st;
@@ -53,8 +54,14 @@ struct DecodeParams {
   int32_t n_work;           // B * Hkv * n_split
   float scale_log2;
 };
-// LDS of decode_combine_kernel (floats): bounds n_split * R * (head_dim + 2).
-constexpr int kCombineLdsFloats = 16384;
+// Workspace layout shared by every plan: kCounterBytes of split counters (decode units, one
+// int32 each; zero at rest) first, then the partials of whichever kernel the plan runs. The
+// counters keep that place whatever plan last used the workspace, so partials never overwrite
+// them and a workspace zeroed once stays usable by every plan.
+constexpr int kCounterSlots = 1024;
+constexpr size_t kCounterBytes = kCounterSlots * sizeof(int32_t);
+// Key splits of one decode unit at most (the merge loops over them).
+constexpr int kMaxDecodeSplits = 64;
 
 struct CombineParams {
   const float* ws;
@@ -87,8 +94,8 @@ hipError_t launch_fwd_f16(const FwdParams& p, int out_dtype, int d, bool kt, int
 hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int variant,
                           hipStream_t s);
 
-// The decode kernel with `waves` (4 or 8; 8 only for head_dim 64) waves per workgroup, then the
-// split combine when p.n_split > 1.
+// The decode kernel with `waves` (1, 2, 4 or 8; 8 only for head_dim 64) waves per workgroup;
+// with p.n_split > 1 the unit's last workgroup merges the splits (p.counters zeroed).
 hipError_t launch_decode(const DecodeParams& p, int mode, int out_dtype, int head_dim,
                          bool k_transposed, int waves, hipStream_t stream);
 

@@ -1,6 +1,6 @@
-// Instantiations and launch of the decode kernel (bf16 and f16; head_dim 64 with 4 or 8 waves,
-// head_dim 128 with 4; K given transposed or as rows; f32 or same-type output) and of the
-// split combine.
+// Instantiations and launch of the decode kernel (bf16 and f16; head_dim 64 with 1, 2, 4 or 8
+// waves, head_dim 128 with 1, 2 or 4; K given transposed or as rows; f32 or same-type output).
+// Split units merge inside the same launch (the unit's last workgroup), so a call is one launch.
 #include "decode_kernels.cuh"
 
 namespace ffai {
@@ -11,15 +11,13 @@ hipError_t launch_dec(const DecodeParams& p, hipStream_t s) {
   const unsigned grid = (unsigned)((p.n_work + 7) / 8 * 8);  // whole XCD rounds
   hipLaunchKernelGGL((decode_kernel<MODE, OUTT, D, KT, NWD>), dim3(grid), dim3(NWD * 64), 0, s,
                      p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.n_split == 1) return e;
-  hipLaunchKernelGGL((decode_combine_kernel<OUTT, D>), dim3((unsigned)(p.B * p.Hkv)), dim3(256), 0,
-                     s, p);
   return hipGetLastError();
 }
 
 template <int MODE, int OUTT, int D, bool KT>
 hipError_t pick_waves(const DecodeParams& p, int waves, hipStream_t s) {
+  if (waves == 1) return launch_dec<MODE, OUTT, D, KT, 1>(p, s);
+  if (waves == 2) return launch_dec<MODE, OUTT, D, KT, 2>(p, s);
   if (waves == 4) return launch_dec<MODE, OUTT, D, KT, 4>(p, s);
   if constexpr (D == 64) {
     if (waves == 8) return launch_dec<MODE, OUTT, D, KT, 8>(p, s);

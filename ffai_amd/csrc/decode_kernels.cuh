@@ -9,11 +9,11 @@
 //     position -- are the 32 columns of one S^T = K Q^T MFMA block, so K and V are read once
 //     per kv-head however many heads or beams share them;
 //   * the waves' partial (O, max, sum) merge through LDS. When one workgroup covers a unit's
-//     keys (decoder self-attention: up to 8 tiles) it writes the output directly; otherwise
-//     each writes its merged partial and decode_combine_kernel, one workgroup per unit, stages
-//     all of a unit's partials in LDS with one round of loads and merges them. (An in-kernel
-//     last-arriver merge needs a device-scope release per workgroup, which on this GPU writes
-//     back the L2 and serialises: measured slower than the second launch.)
+//     keys it writes the output directly; otherwise each writes its merged partial with
+//     device-scope stores and counts itself on the unit's counter, and the unit's last
+//     workgroup merges every split's partial and writes the output, in the same launch. (A
+//     device-scope release fence per workgroup would write back the whole L2 here; stores that
+//     are themselves device-scope need no fence, only their acknowledgement.)
 //   * each wave's tile region is its own: whole tiles arrive by DMA (global -> LDS, no staging
 //     registers) into unpadded, XOR-swizzled rows, and a wave waits only for its own loads;
 //   * the tile loop is not unrolled: a cold workgroup fetches little code.
@@ -409,53 +409,82 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     if (p.n_split == 1) {
       store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
     } else {
-      *reinterpret_cast<f32x4*>(&ws_o[(prow0 + n) * D + 4 * c4]) = acc;
-      if (c4 == 0) *reinterpret_cast<f32x2*>(&ws_ml[(prow0 + n) * 2]) = f32x2{M, L};
+      // This split's partial, written as device-scope stores: each one reaches the device's
+      // coherence point before it is acknowledged, so the unit's last workgroup reads it
+      // wherever (on whichever XCD) it runs, without a write-back of this L2's dirty lines.
+      float* po = &ws_o[(prow0 + n) * D + 4 * c4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        __hip_atomic_store(po + e, acc[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (c4 == 0) {
+        __hip_atomic_store(&ws_ml[(prow0 + n) * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ws_ml[(prow0 + n) * 2 + 1], L, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
-}
+  if (p.n_split == 1) return;
 
-// Merge a unit's split partials: one workgroup per (batch, kv-head) unit stages every split's
-// (O, m, l) rows in LDS (one round of independent loads), then each thread merges one 4-element
-// chunk of one row by log-sum-exp and writes it. The host keeps n_split * R * (D + 2) floats
-// within kCombineLdsFloats.
-template <int OUTT, int D>
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
-  const int unit = blockIdx.x;
-  if (unit >= p.B * p.Hkv) return;
-  const int hk = unit % p.Hkv, b = unit / p.Hkv;
-  const int R = p.group * p.Tq;
-  const int S = p.n_split;
-  __shared__ __attribute__((aligned(16))) float buf[kCombineLdsFloats];
-  const float* so = p.ws + (int64_t)unit * S * R * D;
-  const float* sml = p.ws + (int64_t)p.B * p.Hkv * S * R * D + (int64_t)unit * S * R * 2;
-  const int n_o = S * R * D, n_ml = S * R * 2;
-  const int tid = threadIdx.x;
-  for (int i = 4 * tid; i < n_o; i += 4 * 256)
-    *reinterpret_cast<f32x4*>(&buf[i]) = *reinterpret_cast<const f32x4*>(&so[i]);
-  for (int i = 2 * tid; i < n_ml; i += 2 * 256)
-    *reinterpret_cast<f32x2*>(&buf[n_o + i]) = *reinterpret_cast<const f32x2*>(&sml[i]);
+  // ---- count this split; the unit's last one merges them all.
+  // Ordering: every thread waits for its partial stores to be acknowledged (vmcnt(0): device-
+  // scope stores are acknowledged once they are visible at device scope), the barrier makes that
+  // true of the whole workgroup, and only then does one thread add 1 to the unit's counter (a
+  // device-scope atomic). The workgroup that reads n_split - 1 back is the unit's last: every
+  // other split's partial was visible before its increment, which precedes this one in the
+  // counter's order, and this workgroup's device-scope loads are issued after that increment
+  // returns. The last workgroup sets the counter back to 0 for the next call (no wait anywhere:
+  // a workgroup that is not last simply ends).
+  __shared__ int s_last;
+  vm_wait_all();
   __syncthreads();
-  constexpr int C4 = D / 4;
-  const float* ml = buf + n_o;
+  if (tid == 0) {
+    const int done = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (done == p.n_split - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int S = p.n_split;
+  const float* uo = ws_o + (int64_t)unit * S * R * D;
+  const float* uml = ws_ml + (int64_t)unit * S * R * 2;
+  // Online log-sum-exp merge over the splits, eight at a time: the eight splits' loads are
+  // issued together (clamped to the last split; those past it count as empty), then merged in
+  // split order, so one round trip covers eight partials.
+  constexpr int KS = 8;
 #pragma unroll 1
-  for (int it = tid; it < R * C4; it += 256) {
+  for (int it = tid; it < items; it += NWD * 64) {
     const int n = it / C4, c4 = it % C4;
-    float M = kNegInf;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[(s * R + n) * 2]);
-    const float Mc = (M == kNegInf) ? 0.f : M;
+    float M = kNegInf, L = 0.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float L = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) {
-      const int row = s * R + n;
-      const float wt = fast_exp2(ml[row * 2] - Mc);
-      acc += wt * *reinterpret_cast<const f32x4*>(&buf[row * D + 4 * c4]);
-      L = __builtin_fmaf(wt, ml[row * 2 + 1], L);
+#pragma unroll 1
+    for (int s0 = 0; s0 < S; s0 += KS) {
+      float mj[KS], lj[KS];
+      f32x4 xj[KS];
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const int row = min(s0 + j, S - 1) * R + n;
+        mj[j] = __hip_atomic_load(&uml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lj[j] = __hip_atomic_load(&uml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          xj[j][e] = __hip_atomic_load(&uo[row * D + 4 * c4 + e], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const float m = (s0 + j < S) ? mj[j] : kNegInf;
+        const float m_new = fmaxf(M, m);
+        if (m_new == kNegInf) continue;  // nothing seen yet (every key so far masked)
+        const float c_old = fast_exp2(M - m_new);  // 0 while M is -inf
+        const float c_new = fast_exp2(m - m_new);  // 0 for an empty split
+        acc = acc * c_old + xj[j] * c_new;
+        L = L * c_old + lj[j] * c_new;
+        M = m_new;
+      }
     }
     store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
   }
+  if (tid == 0) __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace

@@ -64,7 +64,8 @@ class EncoderAttention:
         if workspace is None:
             need = self.workspace_bytes(x)
             if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
-                self._ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+                # zeroed once: it holds the attention's split counters (left zero by each call)
+                self._ws = torch.zeros(need, dtype=torch.uint8, device=x.device)
             workspace = self._ws
         if out is None:
             out = torch.empty_like(x)

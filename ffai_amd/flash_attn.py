@@ -53,7 +53,7 @@ def _view(t: torch.Tensor) -> L.TensorView:
 def _workspace(nbytes: int, device) -> torch.Tensor | None:
     if nbytes == 0:
         return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)  # counters start at zero
 
 
 # -------------------------------------------------------------------------------------------

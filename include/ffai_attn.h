@@ -27,9 +27,11 @@
  * streams may be used concurrently from distinct threads. Element strides are in ELEMENTS.
  *
  * Workspace: shapes that split the keys over workgroups need a device workspace of
- * *_workspace_bytes bytes (16-byte aligned) for the partial results; its contents need no
- * initialisation. A workspace belongs to one call at a time: calls that may overlap (different
- * streams) need their own; stream-ordered calls and captured HIP graphs may share one.
+ * *_workspace_bytes bytes (16-byte aligned) for split counters and partial results. Zero it
+ * once, before its first use (hipMemset at allocation, or torch.zeros); every call leaves its
+ * counters zero again, so a workspace zeroed once serves any number of calls of any shapes. A
+ * workspace belongs to one call at a time: calls that may overlap (different streams) need
+ * their own; stream-ordered calls and captured HIP graphs may share one.
  */
 #ifndef FFAI_ATTN_H
 #define FFAI_ATTN_H
@@ -92,7 +94,8 @@ void ffai_attn_desc_init(ffai_attn_desc* d, int32_t q_dtype, int32_t kv_dtype,
  * (the failure flash_attn.rs:113-125 documents). */
 int ffai_attn_serves(const ffai_attn_desc* d);
 
-/* Device workspace ffai_attn_fwd needs for this descriptor (split-key partials); 0 if none. */
+/* Device workspace ffai_attn_fwd needs for this descriptor (split counters and split-key
+ * partials; zeroed once before first use, see above); 0 if none. */
 int ffai_attn_workspace_bytes(const ffai_attn_desc* d, size_t* bytes);
 
 /* O = softmax(scale * Q K^T [+ causal mask]) V. Returns FFAI_DECLINED for descriptors
@@ -174,6 +177,12 @@ int ffai_attend_merged_workspace_bytes(const ffai_tensor* q, const ffai_tensor* 
  * decode shape declines. Initialised from FFAI_DECODE_MIN_KEYS (default 8) on first use. */
 int ffai_get_decode_min_keys(void);
 void ffai_set_decode_min_keys(int n);
+
+/* Tuning knob, no counterpart in the reference: 64-key tiles per workgroup of the decode kernel
+ * (0 = the planner's choice). Initialised from FFAI_DECODE_TILES_PER_WG on first use. It changes
+ * how a decode call splits its keys over workgroups, never its result beyond f32 rounding. */
+int ffai_get_decode_tiles_per_wg(void);
+void ffai_set_decode_tiles_per_wg(int n);
 
 /* Human-readable description of the last error on the calling thread ("" if none). */
 const char* ffai_attn_last_error(void);

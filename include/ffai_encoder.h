@@ -66,7 +66,8 @@ typedef struct ffai_encoder_attn_weights {
 int ffai_encoder_attn_workspace_bytes(const ffai_encoder_attn_desc* d, size_t* bytes);
 
 /* x: (batch, seq, n_state) row-major; out: the same shape. workspace: at least
- * ffai_encoder_attn_workspace_bytes(d), 256-byte aligned; its contents need no initialisation. */
+ * ffai_encoder_attn_workspace_bytes(d), 256-byte aligned, zeroed once before its first use (it
+ * holds the attention's split counters, which every call leaves zero). */
 int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
                           const ffai_encoder_attn_weights* w, void* out, void* workspace,
                           size_t workspace_bytes, void* stream);

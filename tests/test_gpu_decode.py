@@ -11,6 +11,7 @@ import pytest
 import torch
 
 import oracle
+from ffai_amd import _lib as L
 from ffai_amd import flash_attn as fa
 from tests.helpers import TOL_BF16, max_abs, randn, round_bf16, round_f16
 
@@ -199,10 +200,15 @@ def _beam_cross_inputs(rng, gpu, beams=5, h=16, t=1500, d=64):
     return q, kt, v, _dev(q, torch.bfloat16, gpu), _dev(kt, torch.bfloat16, gpu), _dev(v, torch.bfloat16, gpu)
 
 
+COUNTER_BYTES = 4096  # the split counters at the workspace's start
+
+
 def test_workspace_reuse_and_graph_replays(gpu):
-    """One workspace serves repeated eager calls and every replay of a captured HIP graph (with
-    eager work and synchronisation between replays): each result matches the first eager one
-    exactly and the oracle within tolerance."""
+    """One workspace, zeroed once, serves repeated eager calls and every replay of a captured HIP
+    graph (with eager work and synchronisation between replays): each result matches the first
+    eager one exactly and the oracle within tolerance, and the split counters are back at zero
+    after every call. Past the counters the workspace starts as garbage (0xFF): partials are
+    written before they are read."""
     rng = np.random.default_rng(2024)
     q, kt, v, qd, ktd, vd = _beam_cross_inputs(rng, gpu)
     beams, h, _, d = q.shape
@@ -210,7 +216,8 @@ def test_workspace_reuse_and_graph_replays(gpu):
     args = dict(k_transposed=True, scale=0.125)
     nbytes = fa.workspace_bytes(qd.permute(2, 1, 0, 3), ktd, vd, out.permute(2, 1, 0, 3), **args)
     assert nbytes > 0
-    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=gpu)  # no initialisation needed
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=gpu)
+    ws[:COUNTER_BYTES].zero_()
 
     def call():
         fa.attention(qd.permute(2, 1, 0, 3), ktd, vd, out=out.permute(2, 1, 0, 3),
@@ -228,6 +235,7 @@ def test_workspace_reuse_and_graph_replays(gpu):
         call()
         torch.cuda.synchronize()
         assert torch.equal(out, first)
+        assert not ws[:COUNTER_BYTES].any()
 
     graph = torch.cuda.CUDAGraph()
     out.zero_()
@@ -240,6 +248,49 @@ def test_workspace_reuse_and_graph_replays(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, first), f"replay {i} differs"
+        assert not ws[:COUNTER_BYTES].any(), f"replay {i} left a counter set"
+
+
+@pytest.fixture
+def tiles_knob():
+    lib = L.load()
+    yield lib.ffai_set_decode_tiles_per_wg
+    lib.ffai_set_decode_tiles_per_wg(0)
+
+
+@pytest.mark.parametrize("tiles_per_wg", [1, 3, 24])
+def test_split_merge_never_reads_stale_partials(gpu, tiles_per_wg, tiles_knob):
+    """Two beam-5 cross-attention problems alternate 12 times on one workspace. Each call's last
+    workgroup merges partials the same call wrote; a stale partial (the other problem's) would
+    change the output, so every call must equal its problem's first result bit for bit, for
+    splits of 1, 3 and 24 tiles (24, 8 and 1 workgroups per head)."""
+    rng = np.random.default_rng(77)
+    cases = [_beam_cross_inputs(rng, gpu), _beam_cross_inputs(rng, gpu)]
+    beams, h, _, d = cases[0][0].shape
+    args = dict(k_transposed=True, scale=0.125)
+    outs = [torch.empty(beams, h, 1, d, dtype=torch.float32, device=gpu) for _ in cases]
+    nbytes = fa.workspace_bytes(cases[0][3].permute(2, 1, 0, 3), cases[0][4], cases[0][5],
+                                outs[0].permute(2, 1, 0, 3), **args)
+    tiles_knob(tiles_per_wg)
+    nbytes = max(nbytes, fa.workspace_bytes(cases[0][3].permute(2, 1, 0, 3), cases[0][4],
+                                            cases[0][5], outs[0].permute(2, 1, 0, 3), **args))
+    ws = torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=gpu)
+    first = [None, None]
+    for i in range(24):
+        c = i % 2
+        _, _, _, qd, ktd, vd = cases[c]
+        outs[c].zero_()
+        fa.attention(qd.permute(2, 1, 0, 3), ktd, vd, out=outs[c].permute(2, 1, 0, 3),
+                     workspace=ws, **args)
+        torch.cuda.synchronize()
+        if first[c] is None:
+            q, kt, v = cases[c][:3]
+            want = np.swapaxes(oracle.attend_general(np.swapaxes(q, 0, 2), kt, v, **args), 0, 2)
+            assert max_abs(_host(outs[c]), want) < TOL_BF16
+            first[c] = outs[c].clone()
+        else:
+            assert torch.equal(outs[c], first[c]), f"call {i} differs"
+    assert not ws[:COUNTER_BYTES].any()
 
 
 def test_two_calls_share_nothing_but_the_workspace(gpu):
@@ -254,7 +305,7 @@ def test_two_calls_share_nothing_but_the_workspace(gpu):
     o2 = torch.empty_like(o1)
     n = max(fa.workspace_bytes(qd1.permute(2, 1, 0, 3), ktd1, vd1, o1.permute(2, 1, 0, 3), **args),
             fa.workspace_bytes(qd2.permute(2, 1, 0, 3), ktd2, vd2, o2.permute(2, 1, 0, 3), **args))
-    ws = torch.empty(n, dtype=torch.uint8, device=gpu)
+    ws = torch.zeros(n, dtype=torch.uint8, device=gpu)
     fa.attention(qd1.permute(2, 1, 0, 3), ktd1, vd1, out=o1.permute(2, 1, 0, 3), workspace=ws, **args)
     fa.attention(qd2.permute(2, 1, 0, 3), ktd2, vd2, out=o2.permute(2, 1, 0, 3), workspace=ws, **args)
     w1 = np.swapaxes(oracle.attend_general(np.swapaxes(q1, 0, 2), kt1, v1, **args), 0, 2)

@@ -252,7 +252,7 @@ def test_append_and_attend_replay_in_a_graph(gpu):
     nv = torch.empty_like(nk)
     q = torch.empty(beams, heads, 1, d, dtype=torch.bfloat16, device=gpu)
     out = torch.empty(beams, heads, 1, d, dtype=torch.float32, device=gpu)
-    ws = torch.empty(max(1, fa.workspace_bytes(q, g_cache.k, g_cache.v, out, scale=scale,
+    ws = torch.zeros(max(1, fa.workspace_bytes(q, g_cache.k, g_cache.v, out, scale=scale,
                                                kv_lens=g_cache.lens)), dtype=torch.uint8, device=gpu)
 
     def step(cache):

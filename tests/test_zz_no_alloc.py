@@ -33,7 +33,7 @@ def _both(lib, q, k, v, **kw):
     d = _desc(q, k, v, o_ws, **kw)
     n = ctypes.c_size_t(0)
     assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == L.FFAI_OK
-    ws = torch.empty(max(n.value, 16), dtype=torch.uint8, device=q.device)
+    ws = torch.zeros(max(n.value, 16), dtype=torch.uint8, device=q.device)
     stream = fa._stream_handle()
     rc = lib.ffai_attn_fwd(ctypes.byref(d), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                            o_ws.data_ptr(), ws.data_ptr(), ws.numel(), stream)
