@@ -18,7 +18,8 @@ the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this ho
 bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras] [--eager]
-                       [--layers L] [--legs decode,state,block,gemv,tiny,small,prefill | none | copy]
+                       [--layers L] [--legs decode,state,block,gemv,tiny,small,prefill,floor | none
+                       | copy]
 """
 
 from __future__ import annotations
@@ -47,10 +48,10 @@ def parse():
     ap.add_argument("--eager", action="store_true",
                     help="decode leg without HIP graphs (for counter collection)")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill",
+    ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill,floor",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "state, block, gemv, tiny, small, prefill, or 'none'; 'copy' alone runs only the copy "
-                         "calibration used to scale HBM byte counters")
+                         "state, block, gemv, tiny, small, prefill, floor, or 'none'; 'copy' alone "
+                         "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
 
 
@@ -146,6 +147,66 @@ def copy_bench(torch, steps, nbytes=1 << 30):
     ms = e0.elapsed_time(e1) / steps
     return {"bytes_each_way": nbytes, "us_per_copy": ms * 1e3,
             "gbps": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
+# ------------------------------------------------------------------------------------------
+# Launch floor: what one launch costs with nothing, or only a bare read, inside it
+# ------------------------------------------------------------------------------------------
+
+def floor_bench(torch, steps=50, launches=24, nbytes=6_175_744, sets=3, workgroups=(128, 256, 512)):
+    """Per-launch time of an empty kernel and of a bare streaming read of `nbytes` (the
+    cross-attention K/V of one whisper-medium layer), each in HIP graphs of `launches` launches
+    as a decode step replays them. Reads rotate over `sets` x `launches` distinct regions
+    (> 2 x the 256 MB MALL), so every launch reads HBM."""
+    import ctypes
+    from ffai_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    regions = sets * launches
+    buf = torch.zeros(regions * nbytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(1024, dtype=torch.float32, device=dev)
+
+    def timed(body):
+        graphs = []
+        for st in range(sets):
+            body(st)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                body(st)
+            graphs.append(gr)
+        for i in range(5):
+            graphs[i % sets].replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            graphs[i % sets].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (steps * launches)
+
+    def stream():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def empty(_st):
+        for _ in range(launches):
+            _lib.check(lib.ffai_probe_empty(128, stream()))
+
+    res = {"launches_per_graph": launches, "bytes_per_read": nbytes,
+           "empty_us": timed(empty), "read_us": {}, "read_gbps": {}}
+    for wg in workgroups:
+        def read(st, wg=wg):
+            for i in range(launches):
+                off = (st * launches + i) * nbytes
+                _lib.check(lib.ffai_probe_read(buf.data_ptr() + off, nbytes, out.data_ptr(), wg,
+                                               stream()))
+        us = timed(read)
+        res["read_us"][str(wg)] = us
+        res["read_gbps"][str(wg)] = nbytes / (us * 1e-6) / 1e9
+    return res
 
 
 # ------------------------------------------------------------------------------------------
@@ -512,47 +573,100 @@ def gemv_bench(torch, steps, warmup, beams=5, n=1024, layers=24, vocab=51865):
 # CPU baseline: the oracle (reference algorithm restated) on this host's cores
 # ------------------------------------------------------------------------------------------
 
-def cpu_baseline(H=20, T=1500, D=64, budget_s=12.0):
+def host_info():
+    """CPUs this process may run on (sched_getaffinity) and the CPU model."""
+    cpus = len(os.sched_getaffinity(0))
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return cpus, model
+
+
+def cpu_baselines(rounds=21):
+    """The reference's kernel, restated by the oracle in C++/AVX2, timed on this host on each
+    encoder-shaped workload, by the reference's own method (examples/flash_probe.rs:409-432):
+    one warm-up, then `rounds` interleaved rounds (each round runs every workload once, the order
+    reversed on odd rounds), the median per workload. Threads: one per head up to the host's
+    CPUs, as rayon spreads the heads (flash_attn.rs:199,402); batch items run serially, as the
+    reference loops them (text_decoder.rs:1069-1076). Inputs are bf16-rounded where the GPU leg
+    is bf16 (the reference computes in f32 on those values). The causal GQA prefill has no
+    reference path: it runs the oracle's extension of the same tiling (labelled so)."""
     import numpy as np
 
     import oracle
 
     oracle.build()
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    cpus, model = host_info()
+    rb = oracle.round_bf16
+
+    def rnd(rng, shape, mult=1.0):
+        return (rng.standard_normal(shape) * mult).astype(np.float32)
+
+    work = {}
+    # whisper-large-v3 (headline): one batch item of one layer, 20 heads
     rng = np.random.default_rng(4)
-    q = oracle.round_bf16(rng.standard_normal((1, H, T, D)).astype(np.float32)) * np.float32(0.125)
-    kt = oracle.round_bf16(rng.standard_normal((1, H, D, T)).astype(np.float32))
-    v = oracle.round_bf16(rng.standard_normal((1, H, T, D)).astype(np.float32))
-    oracle.attend_f32(q, kt, v, threads=threads)  # warm-up
-    times = []
+    q, kt, v = rb(rnd(rng, (1, 20, 1500, 64))) * np.float32(0.125), rb(rnd(rng, (1, 20, 64, 1500))), rb(rnd(rng, (1, 20, 1500, 64)))
+    work["encoder_large_v3"] = dict(
+        run=lambda q=q, kt=kt, v=v: oracle.attend_f32(q, kt, v, threads=min(cpus, 20)),
+        flop=4.0 * 20 * 1500 ** 2 * 64, threads=min(cpus, 20), kind="port",
+        sample="one batch item (20 heads x T=1500, D=64) of one whisper-large-v3 layer, bf16-rounded "
+               "inputs in f32 math; the reference runs the 16 items serially, so this is the "
+               "layer's rate")
+    # whisper-tiny f32: the 4 layers, 6 heads each
+    rng = np.random.default_rng(1)
+    tiny = [(rnd(rng, (1, 6, 1500, 64)) * np.float32(0.125), rnd(rng, (1, 6, 64, 1500)),
+             rnd(rng, (1, 6, 1500, 64))) for _ in range(4)]
+    work["encoder_tiny_f32"] = dict(
+        run=lambda: [oracle.attend_f32(a, b, c, threads=min(cpus, 6)) for a, b, c in tiny],
+        flop=4 * 4.0 * 6 * 1500 ** 2 * 64, threads=min(cpus, 6), kind="port",
+        sample="the 4 whisper-tiny encoder layers (6 heads x T=1500, D=64, f32)")
+    # whisper-small f32: 8 items serially, 12 heads each, K x 2
+    rng = np.random.default_rng(2)
+    small = [(rnd(rng, (1, 12, 1500, 64)) * np.float32(0.125), rnd(rng, (1, 12, 64, 1500), 2.0),
+              rnd(rng, (1, 12, 1500, 64))) for _ in range(8)]
+    work["encoder_small_f32"] = dict(
+        run=lambda: [oracle.attend_f32(a, b, c, threads=min(cpus, 12)) for a, b, c in small],
+        flop=8 * 4.0 * 12 * 1500 ** 2 * 64, threads=min(cpus, 12), kind="port",
+        sample="one whisper-small layer: 8 batch items serially, 12 heads x T=1500, D=64, f32, "
+               "K x 2")
+    # Qwen2-VL causal GQA prefill: the oracle's extension (no reference path)
+    rng = np.random.default_rng(5)
+    S = 4096
+    pq, pk, pv = rb(rnd(rng, (1, 12, S, 128))), rb(rnd(rng, (1, 2, S, 128))), rb(rnd(rng, (1, 2, S, 128)))
+    work["prefill_causal_gqa_d128"] = dict(
+        run=lambda: oracle.attend_general(pq, pk, pv, k_transposed=False, scale=128 ** -0.5,
+                                          causal=True, threads=min(cpus, 12)),
+        flop=4.0 * 12 * 128 * S * (S + 1) / 2, threads=min(cpus, 12), kind="oracle, not reference",
+        sample="causal GQA prefill Hq12 over Hkv2, D=128, S=4096, bf16-rounded inputs in f32 math; "
+               "the reference has no such path, so this times the oracle's extension of its tiling")
+    names = list(work)
+    for n in names:  # warm-up
+        work[n]["run"]()
+    times = {n: [] for n in names}
     t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or len(times) < 3:
-        t0 = time.perf_counter()
-        oracle.attend_f32(q, kt, v, threads=threads)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 41:
-            break
-    med = float(np.median(times))
-    flop = 4.0 * H * T * T * D
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {
-        "value": flop / med / 1e12,
-        "unit": "TFLOP/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"one batch item of one whisper-large-v3 encoder layer: {H} heads x T={T}, "
-                   f"D={D}, bf16-rounded inputs in f32 math (the reference kernel's dtype); "
-                   f"median of {len(times)} runs, {med * 1e3:.1f} ms each; "
-                   f"heads over {threads} threads as rayon does; CPU: {cpu_model}"),
-    }
+    for r in range(rounds):
+        for n in (names if r % 2 == 0 else names[::-1]):
+            t0 = time.perf_counter()
+            work[n]["run"]()
+            times[n].append(time.perf_counter() - t0)
+    total_s = time.perf_counter() - t_start
+    out = {}
+    for n in names:
+        med = float(np.median(times[n]))
+        w = work[n]
+        out[n] = {"value": w["flop"] / med / 1e12, "unit": "TFLOP/s", "cores": w["threads"],
+                  "host_cpus": cpus, "cpu_model": model, "kind": w["kind"], "ms": med * 1e3,
+                  "sample": (f"{w['sample']}; median of {rounds} interleaved rounds after one "
+                             f"warm-up ({med * 1e3:.1f} ms each; the {len(names)} workloads' "
+                             f"rounds took {total_s:.1f} s); heads over {w['threads']} of the "
+                             f"host's {cpus} CPUs; CPU: {model}")}
+    return out
 
 
 def cpu_decode_baseline(beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24, reps=5):
@@ -568,7 +682,8 @@ def cpu_decode_baseline(beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24, rep
     import oracle
 
     oracle.build()
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    cpus, model = host_info()
+    threads = min(cpus, H)  # the heads-parallel arm: one head per thread, up to the host's CPUs
     g = torch.Generator(device="cpu").manual_seed(3)  # the GPU decode leg's cache lengths
     lens = torch.randint(1, cap + 1, (layers, beams), generator=g, dtype=torch.int32).numpy()
     rng = np.random.default_rng(3)
@@ -597,10 +712,13 @@ def cpu_decode_baseline(beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24, rep
         self_s = time.perf_counter() - t0
         out[f"us_per_step_{name}"] = (float(np.median(cross)) * layers + self_s) * 1e6
     out["threads"] = threads
+    out["host_cpus"] = cpus
+    out["cpu_model"] = model
     out["kind"] = "port"
     out["sample"] = (f"one layer's {beams} cross-attention calls (f16 K/V, {H} heads x {T_enc} "
                      f"frames), median of {reps}, x {layers} layers; plus all {layers * beams} "
-                     f"self-attention calls (f32 caches, the GPU leg's lengths)")
+                     f"self-attention calls (f32 caches, the GPU leg's lengths); heads-parallel "
+                     f"arm on a persistent pool of {threads} threads, as rayon's")
     return out
 
 
@@ -675,6 +793,12 @@ def main():
         small["frac_of_bf16_peak"] = small["tflops"] / PEAK_BF16_TFLOPS
         extras["encoder_small_bf16"] = small
         log(f"small bf16: {small['tflops']:.1f} TFLOP/s")
+        log("encoder: whisper-small f32 ...")
+        small32 = encoder_bench(torch, fa, args.steps, args.warmup, 4, B=8, H=12, seed=2,
+                                k_mult=2.0, dtype="f32")
+        small32["frac_of_f32_peak"] = small32["tflops"] / PEAK_F32_TFLOPS
+        extras["encoder_small_f32"] = small32
+        log(f"small f32: {small32['tflops']:.2f} TFLOP/s")
     if "prefill" in legs:
         log("prefill: qwen2-vl causal GQA bf16 ...")
         pre = encoder_bench(torch, fa, args.steps, args.warmup, 4, B=1, H=12, H_kv=2, T=4096,
@@ -682,11 +806,24 @@ def main():
         pre["frac_of_bf16_peak"] = pre["tflops"] / PEAK_BF16_TFLOPS
         extras["prefill_causal_gqa_d128"] = pre
         log(f"prefill: {pre['tflops']:.1f} TFLOP/s")
+    if "floor" in legs:
+        log("launch floor: empty kernel and bare 6 MB reads in graphs ...")
+        fl = floor_bench(torch)
+        log(f"launch floor: empty {fl['empty_us']:.2f} us, 6 MB read "
+            + ", ".join(f"{k} WGs {v:.2f} us" for k, v in fl["read_us"].items()))
+        extras["launch_floor"] = fl
     cpu = None
     if not args.skip_cpu:
-        log("cpu baseline ...")
-        cpu = cpu_baseline()
+        log("cpu baselines (oracle restating the reference's kernel) ...")
+        cpus = cpu_baselines()
+        cpu = cpus["encoder_large_v3"]
         log(f"cpu: {cpu['value'] * 1e3:.1f} GFLOP/s on {cpu['cores']} threads")
+        for name, leg in (("encoder_tiny_f32", "encoder_tiny_f32"),
+                          ("encoder_small_f32", "encoder_small_f32"),
+                          ("prefill_causal_gqa_d128", "prefill_causal_gqa_d128")):
+            extras.setdefault(leg, {})["cpu"] = cpus[name]
+            log(f"cpu {name}: {cpus[name]['value'] * 1e3:.1f} GFLOP/s on {cpus[name]['cores']} "
+                f"threads")
         if "decode_beam5" in extras:
             dcpu = cpu_decode_baseline()
             extras["decode_beam5"]["cpu"] = dcpu
@@ -717,6 +854,13 @@ def main():
                      "traffic": load_traffic("encoder_large_v3_bf16")},
         "cpu_baseline": cpu,
     }
+    if "decode_beam5" in extras:
+        dec = extras["decode_beam5"]
+        line["roofline_decode"] = {"bound": "hbm", "achieved": round(dec["gbps"], 1),
+                                   "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                                   "frac": round(dec["gbps"] / PEAK_HBM_GBPS, 4),
+                                   "us_per_step": round(dec["us_per_step"], 1),
+                                   "traffic": load_traffic("decode_beam5")}
     if extras:
         line["extras"] = extras
     print(json.dumps(line), flush=True)

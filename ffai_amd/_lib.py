@@ -135,7 +135,10 @@ def load():
     L.ffai_vocab_int8_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_vocab_int8_logits.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, i64, vp,
                                          ctypes.c_size_t, vp]
-    for name in ("ffai_attn_serves", "ffai_attn_workspace_bytes", "ffai_attn_fwd",
+    L.ffai_probe_empty.argtypes = [ctypes.c_int, vp]
+    L.ffai_probe_read.argtypes = [vp, sz, vp, ctypes.c_int, vp]
+    for name in ("ffai_probe_empty", "ffai_probe_read", "ffai_attn_serves",
+                 "ffai_attn_workspace_bytes", "ffai_attn_fwd",
                  "ffai_attn_plan_info", "ffai_attn_fwd_noalloc", "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",

@@ -1,9 +1,11 @@
 """Build the gfx950 attention library in-tree: ffai_amd/libffai_attn.so.
 
 hipcc compiles the kernel instantiations (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip, decode.hip),
-the decode-state kernels and their C ABI (kv_cache.hip), the launch dispatch (attn_launch.hip),
-the attention C ABI (attn_api.cpp) and the encoder attention block around hipBLASLt
-(encoder_attn.cpp) for gfx950 only, in parallel, then links them into one shared library. Packed-FP32 VALU instructions are disabled for all device code.
+the decode-state kernels and their C ABI (kv_cache.hip), the decoder GEMVs (gemv.hip), the
+launch-floor probes (probe.hip), the launch dispatch (attn_launch.hip), the attention C ABI
+(attn_api.cpp) and the encoder attention block around hipBLASLt (encoder_attn.cpp) for gfx950
+only, in parallel, then links them into one shared library. Packed-FP32 VALU instructions are
+disabled for all device code.
 """
 
 from __future__ import annotations
@@ -20,7 +22,7 @@ LIB_PATH = os.path.join(HERE, "libffai_attn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = [os.path.join(CSRC, n) for n in
            ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "kv_cache.hip",
-            "gemv.hip", "attn_launch.hip", "attn_api.cpp", "encoder_attn.cpp")]
+            "gemv.hip", "probe.hip", "attn_launch.hip", "attn_api.cpp", "encoder_attn.cpp")]
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 ARCH = "gfx950"
 

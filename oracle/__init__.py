@@ -32,7 +32,7 @@ from . import textbook  # noqa: F401  (re-export)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
-_VERSION = 4
+_VERSION = 5
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u16p = ctypes.POINTER(ctypes.c_uint16)

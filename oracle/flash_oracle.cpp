@@ -25,8 +25,14 @@
 #include <algorithm>
 #include <cmath>
 #include <limits>
+#include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
 #include <thread>
 #include <vector>
+
+#include <sched.h>
 
 namespace {
 
@@ -311,21 +317,79 @@ __attribute__((target("avx2,fma,f16c"))) void decode_head(const float* q,
   for (int c = 0; c < 8; ++c) _mm256_storeu_ps(out + 8 * c, a[c]);
 }
 
-// Fan `n` independent jobs over up to `threads` OS threads (the reference uses rayon's pool).
+// A persistent pool of worker threads, as rayon's global pool (the reference's `par_iter`s,
+// flash_attn.rs:199,402): created on first use with as many workers as the process may run on,
+// then reused by every call, so a call pays a wake-up and no thread creation. parallel_for(n,
+// threads, f) runs f(0..n-1) on up to `threads` threads (the caller is one of them); jobs are
+// handed out in index order through an atomic counter. Calls are serialised (one at a time).
+class Pool {
+ public:
+  static Pool& get() {
+    static Pool* p = new Pool();  // never destroyed: the workers live as long as the process
+    return *p;
+  }
+  template <class F>
+  void run(int n, int threads, F&& f) {
+    std::lock_guard<std::mutex> call(call_mu_);
+    threads = std::max(1, std::min({threads, n, (int)workers_.size() + 1}));
+    if (threads == 1) {
+      for (int i = 0; i < n; ++i) f(i);
+      return;
+    }
+    std::function<void(int)> job = [&f](int i) { f(i); };
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      job_ = &job;
+      n_ = n;
+      next_.store(0);
+      helpers_ = threads - 1;
+      running_ = threads - 1;
+      ++generation_;
+    }
+    cv_.notify_all();
+    drain();
+    std::unique_lock<std::mutex> lk(mu_);
+    done_cv_.wait(lk, [&] { return running_ == 0; });
+    job_ = nullptr;
+  }
+
+ private:
+  Pool() {
+    int nw = 1;
+    cpu_set_t set;
+    if (sched_getaffinity(0, sizeof(set), &set) == 0) nw = std::max(1, CPU_COUNT(&set));
+    for (int w = 0; w < nw - 1; ++w) workers_.emplace_back([this, w] { loop(w); });
+    for (auto& t : workers_) t.detach();
+  }
+  void drain() {
+    for (int i = next_.fetch_add(1); i < n_; i = next_.fetch_add(1)) (*job_)(i);
+  }
+  void loop(int w) {
+    long seen = 0;
+    for (;;) {
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return generation_ != seen; });
+        seen = generation_;
+        if (w >= helpers_) continue;  // this call wants fewer threads
+      }
+      drain();
+      std::lock_guard<std::mutex> lk(mu_);
+      if (--running_ == 0) done_cv_.notify_one();
+    }
+  }
+  std::vector<std::thread> workers_;
+  std::mutex call_mu_, mu_;
+  std::condition_variable cv_, done_cv_;
+  std::function<void(int)>* job_ = nullptr;
+  std::atomic<int> next_{0};
+  int n_ = 0, helpers_ = 0, running_ = 0;
+  long generation_ = 0;
+};
+
 template <class F>
 void parallel_for(int n, int threads, F&& f) {
-  threads = std::max(1, std::min(threads, n));
-  if (threads == 1) {
-    for (int i = 0; i < n; ++i) f(i);
-    return;
-  }
-  std::vector<std::thread> pool;
-  pool.reserve(threads);
-  for (int w = 0; w < threads; ++w)
-    pool.emplace_back([&, w] {
-      for (int i = w; i < n; i += threads) f(i);
-    });
-  for (auto& t : pool) t.join();
+  Pool::get().run(n, threads, f);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -393,7 +457,7 @@ __attribute__((target("avx2,fma"))) void general_head(const float* q, long q_row
 extern "C" {
 
 // Version tag so a stale build is detectable from Python.
-int oracle_version() { return 4; }
+int oracle_version() { return 5; }
 
 // Test hook: plant one of the mistakes listed at g_fault (0 restores the faithful oracle).
 void oracle_plant_fault(int kind) { g_fault = kind; }
