@@ -42,6 +42,13 @@ constexpr float kFastMaxHiF16 = 15.0f;
 template <int DT>
 using store_t = std::conditional_t<DT == kF32, float, uint16_t>;
 
+// Cache-policy operand of the buffer load/store builtins: SC1 set, i.e. device scope (the access
+// is coherent at the device level: stores reach the coherence point before they are
+// acknowledged, loads do not hit a stale copy in a non-coherent cache).
+constexpr int kDeviceScope = 16;
+// Fourth dword of a raw (unformatted, stride 0) buffer resource on this GPU.
+constexpr int kBufferWord3 = 0x00020000;
+
 // ---------------------------------------------------------------------------------------------
 // Conversions.
 // ---------------------------------------------------------------------------------------------

@@ -308,16 +308,22 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
         sacc[st] = mfma16<MODE>(a, qf[s], sacc[st]);
       }
     }
-    // ---- mask, max, rescale, weights
+    // ---- mask (only tiles that reach past a row's last visible key: the ragged end, or the
+    //      causal diagonal of the unit's first row), max, rescale, weights
+    if (kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset)) {  // wave-uniform
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * st + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key > lim) sacc[st][r] = kNegInf;
+        }
+    }
     float mx = kNegInf;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + 32 * st + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key > lim) sacc[st][r] = kNegInf;
-        mx = fmaxf(mx, sacc[st][r]);
-      }
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[st][r], sacc[st][r + 1]));
     const float m_new = fmaxf(m_s, partner_max(mx) * sl2);
     const float corr = (m_new == kNegInf) ? 1.f : fast_exp2(m_s - m_new);
     m_s = m_new;
@@ -383,8 +389,12 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   constexpr int C4 = D / 4;  // 4-float chunks per row
   const int items = R * C4;
   const int64_t prow0 = ((int64_t)unit * p.n_split + split) * R;  // this split's first partial row
-  float* ws_o = p.ws;
-  float* ws_ml = p.ws + (int64_t)p.B * p.Hkv * p.n_split * R * D;
+  // the partials: O rows [units][n_split][R][D], then (m, l) pairs [units][n_split][R][2], as a
+  // buffer resource over exactly those bytes (an access past them would read 0 / be dropped)
+  const int64_t o_floats = (int64_t)p.B * p.Hkv * p.n_split * R * D;
+  const int64_t ws_bytes = (o_floats + (int64_t)p.B * p.Hkv * p.n_split * R * 2) * 4;
+  const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      p.ws, (short)0, (int)(p.n_split > 1 ? ws_bytes : 0), kBufferWord3);
 
 #pragma unroll 1
   for (int it = tid; it < items; it += NWD * 64) {
@@ -409,18 +419,16 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     if (p.n_split == 1) {
       store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
     } else {
-      // This split's partial, written as device-scope stores: each one reaches the device's
-      // coherence point before it is acknowledged, so the unit's last workgroup reads it
-      // wherever (on whichever XCD) it runs, without a write-back of this L2's dirty lines.
-      float* po = &ws_o[(prow0 + n) * D + 4 * c4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        __hip_atomic_store(po + e, acc[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (c4 == 0) {
-        __hip_atomic_store(&ws_ml[(prow0 + n) * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&ws_ml[(prow0 + n) * 2 + 1], L, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
+      // This split's partial, written with device-scope (sc1) buffer stores: each one reaches
+      // the device's coherence point before it is acknowledged, so the unit's last workgroup
+      // reads it wherever (on whichever XCD) it runs, without a write-back of this L2's dirty
+      // lines.
+      __builtin_amdgcn_raw_buffer_store_b128(acc, ws_rsrc, (int)(((prow0 + n) * D + 4 * c4) * 4),
+                                             0, kDeviceScope);
+      if (c4 == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(f32x2{M, L}, ws_rsrc,
+                                              (int)((o_floats + (prow0 + n) * 2) * 4), 0,
+                                              kDeviceScope);
     }
   }
   if (p.n_split == 1) return;
@@ -445,11 +453,11 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   __syncthreads();
   if (!s_last) return;
   const int S = p.n_split;
-  const float* uo = ws_o + (int64_t)unit * S * R * D;
-  const float* uml = ws_ml + (int64_t)unit * S * R * 2;
-  // Online log-sum-exp merge over the splits, eight at a time: the eight splits' loads are
-  // issued together (clamped to the last split; those past it count as empty), then merged in
-  // split order, so one round trip covers eight partials.
+  const int64_t uo = (int64_t)unit * S * R * D;               // the unit's first O row (floats)
+  const int64_t uml = o_floats + (int64_t)unit * S * R * 2;   // and its first (m, l) pair
+  // Online log-sum-exp merge over the splits, eight at a time: the eight splits' device-scope
+  // loads are issued together (clamped to the last split; those past it count as empty), then
+  // merged in split order, so one round trip covers eight partials.
   constexpr int KS = 8;
 #pragma unroll 1
   for (int it = tid; it < items; it += NWD * 64) {
@@ -458,27 +466,25 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
     for (int s0 = 0; s0 < S; s0 += KS) {
-      float mj[KS], lj[KS];
+      f32x2 mlj[KS];
       f32x4 xj[KS];
 #pragma unroll
       for (int j = 0; j < KS; ++j) {
         const int row = min(s0 + j, S - 1) * R + n;
-        mj[j] = __hip_atomic_load(&uml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        lj[j] = __hip_atomic_load(&uml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          xj[j][e] = __hip_atomic_load(&uo[row * D + 4 * c4 + e], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+        mlj[j] = __builtin_amdgcn_raw_buffer_load_b64(ws_rsrc, (int)((uml + row * 2) * 4), 0,
+                                                      kDeviceScope);
+        xj[j] = __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, (int)((uo + row * D + 4 * c4) * 4),
+                                                      0, kDeviceScope);
       }
 #pragma unroll
       for (int j = 0; j < KS; ++j) {
-        const float m = (s0 + j < S) ? mj[j] : kNegInf;
+        const float m = (s0 + j < S) ? mlj[j][0] : kNegInf;
         const float m_new = fmaxf(M, m);
         if (m_new == kNegInf) continue;  // nothing seen yet (every key so far masked)
         const float c_old = fast_exp2(M - m_new);  // 0 while M is -inf
         const float c_new = fast_exp2(m - m_new);  // 0 for an empty split
         acc = acc * c_old + xj[j] * c_new;
-        L = L * c_old + lj[j] * c_new;
+        L = L * c_old + mlj[j][1] * c_new;
         M = m_new;
       }
     }
