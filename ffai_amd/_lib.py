@@ -121,6 +121,11 @@ def load():
     L.ffai_get_decode_tiles_per_wg.restype = ctypes.c_int
     L.ffai_set_decode_tiles_per_wg.argtypes = [ctypes.c_int]
     L.ffai_set_decode_tiles_per_wg.restype = None
+    L.ffai_attn_plan_splits.argtypes = [dp, ctypes.POINTER(ctypes.c_int32)]
+    L.ffai_set_fwd_split_override.argtypes = [ctypes.c_int, ctypes.c_int]
+    L.ffai_set_fwd_split_override.restype = None
+    L.ffai_get_fwd_split_override.argtypes = [ctypes.POINTER(ctypes.c_int)] * 2
+    L.ffai_get_fwd_split_override.restype = None
     L.ffai_attn_last_error.restype = ctypes.c_char_p
     cp = ctypes.POINTER(KVCacheView)
     i32, i64 = ctypes.c_int32, ctypes.c_int64
@@ -139,7 +144,8 @@ def load():
     L.ffai_probe_read.argtypes = [vp, sz, vp, ctypes.c_int, vp]
     for name in ("ffai_probe_empty", "ffai_probe_read", "ffai_attn_serves",
                  "ffai_attn_workspace_bytes", "ffai_attn_fwd",
-                 "ffai_attn_plan_info", "ffai_attn_fwd_noalloc", "ffai_serves",
+                 "ffai_attn_plan_info", "ffai_attn_plan_splits", "ffai_attn_fwd_noalloc",
+                 "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
                  "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",
@@ -156,8 +162,23 @@ def plan_info(desc: AttnDesc) -> dict:
     check(load().ffai_attn_plan_info(ctypes.byref(desc), info))
     kernel = "decode" if info[0] == 1 else "fwd"
     shape = info[1] if kernel == "decode" else ("wave1", "wave4", "wave4x2")[info[1]]
-    return {"kernel": kernel, "shape": shape, "splits": info[2], "tiles_per_split": info[3],
-            "workgroups": info[4]}
+    out = {"kernel": kernel, "shape": shape, "splits": info[2], "tiles_per_split": info[3],
+           "workgroups": info[4]}
+    sp = (ctypes.c_int32 * 3)()
+    check(load().ffai_attn_plan_splits(ctypes.byref(desc), sp))
+    out.update(items=sp[0], split_items=(sp[1], sp[2]))
+    return out
+
+
+def set_fwd_split_override(items: int, pieces: int) -> None:
+    """Force which fused-kernel items run as key-split pieces (0, 0: the planner's choice)."""
+    load().ffai_set_fwd_split_override(int(items), int(pieces))
+
+
+def get_fwd_split_override() -> tuple:
+    a, b = ctypes.c_int(), ctypes.c_int()
+    load().ffai_get_fwd_split_override(ctypes.byref(a), ctypes.byref(b))
+    return a.value, b.value
 
 
 def last_error() -> str:

@@ -65,6 +65,13 @@ int decode_min_keys() {
   return v;
 }
 
+// Tuning and test hook, no counterpart in the reference: force which fwd items run as pieces.
+// items > 0: that many items (the last ones of a non-causal grid, the longest ones of a causal
+// grid) in `pieces` pieces each (1: no item split); items < 0: every item; items == 0 or
+// pieces < 1: the planner's choice.
+std::atomic<int> g_split_items{0};
+std::atomic<int> g_split_pieces{0};
+
 // Tuning knob, no counterpart in the reference: 64-key tiles per decode workgroup (0 = the
 // planner's choice). Initialised from FFAI_DECODE_TILES_PER_WG on first use.
 std::atomic<int> g_decode_tps{-1};
@@ -150,9 +157,12 @@ struct Plan {
   int waves;    // decode: waves per workgroup
   int variant;
   int n_qblk;
-  int n_split;
-  int tiles_per_split;
+  int n_split;          // pieces per split unit (decode) or split item (fwd)
+  int tiles_per_split;  // 64-key tiles per piece (fwd: of the longest item)
   int n_work;
+  // fwd: items [split_lo, split_hi) of n_items run as n_split pieces; dispatch sections
+  int n_items, split_lo, split_hi, sec1_work;
+  bool xcd_remap;
   size_t ws_bytes;
 };
 
@@ -210,7 +220,10 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
 
 // `vector_ok`: the operands admit the decode kernel's vector accesses (it has no element-wise
 // path; misaligned decode shapes take fwd_kernel).
-Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok) {
+// `max_ws`: the workspace available; splits the planner makes only for balance are dropped
+// rather than exceed it.
+Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
+               size_t max_ws = SIZE_MAX) {
   Plan p{};
   if (vector_ok && plan_decode(d, allow_split, &p)) return p;
   const int64_t bh = (int64_t)d->batch * d->heads_q;
@@ -239,34 +252,99 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok) {
   if (forced == ffai::kWave1 || forced == ffai::kWave4 ||
       (forced == ffai::kWave4x2 && !f32 && d->head_dim == 64))
     p.variant = forced;
-  const int64_t work = work_of(p.variant);
+  const int64_t items = work_of(p.variant);
   const int bm = ffai::block_m_of(p.variant);
   p.n_qblk = (d->q_len + bm - 1) / bm;
+  p.n_items = (int)items;
   p.n_split = 1;
   p.tiles_per_split = n_tiles;
-  const int64_t waves = work * (p.variant == ffai::kWave1 ? 1 : 4);
+  p.split_lo = p.split_hi = 0;
+  // Short grids run every item in pieces (merged in the launch). Four-wave grids of fewer items
+  // than CUs take up to three, so that about every CU holds a piece: whisper-tiny (6 heads, 72
+  // items) bf16 20.7 us in 3 pieces against 27.0 whole, f32 55.1 against 71.8 in 2 and 87.8 in
+  // 15; a whisper-large-v3 window (20 heads, 240 items) runs best whole: 27.7 us against 31.2 in
+  // 2 and 39.7 in 3. One-wave grids (prompt steps) keep about 512 workgroups (cross-attention of
+  // 228 tokens, 128 items: 19.3 us in 4 pieces against 22.3 in 2 and 26.2 in 8), at most 8 pieces
+  // an item in f32.
   int64_t want = 1;
-  if (f32) want = (4096 + waves - 1) / waves;
-  // Four-wave grids under 256 workgroups split the keys in three: one window of whisper
-  // tiny/small/medium/large-v3 (72-240 workgroups) measured best at 3 splits (tiny 20.2 us
-  // against 24.5 at 8, small 28.5 against 30.4 at 4; more splits cost combine traffic). One-wave
-  // grids (prompt steps) keep about 512 workgroups.
-  else if (work < 256) want = p.variant == ffai::kWave1 ? (512 + work - 1) / work : 3;
-  // FFAI_ATTN_SPLITS (> 0) forces the key splits of a fwd launch: a tuning knob.
+  if (p.variant == ffai::kWave1) {
+    if (items < 512) want = std::min<int64_t>(f32 ? 8 : ffai::kMaxFwdSplits, (512 + items - 1) / items);
+  } else if (items < 256) {
+    want = std::max<int64_t>(1, std::min<int64_t>(3, 256 / items));
+  }
+  // FFAI_ATTN_SPLITS (> 0) forces the pieces of every item: a tuning knob.
   static const int forced_splits = [] {
     const char* e = std::getenv("FFAI_ATTN_SPLITS");
     return e ? std::atoi(e) : 0;
   }();
   if (forced_splits > 0) want = forced_splits;
-  if (allow_split && want > 1 && n_tiles >= 2) {
-    want = std::min<int64_t>(want, n_tiles);
-    p.tiles_per_split = (int)((n_tiles + want - 1) / want);
-    p.n_split = (n_tiles + p.tiles_per_split - 1) / p.tiles_per_split;
+  int64_t lo = 0, hi = want > 1 ? items : 0;
+  bool optional = false;  // a split for balance only
+  if (want == 1 && !f32) {
+    // Long grids split only the items that would leave the GPU partly idle at the end.
+    // Resident workgroups: four-wave x 64 rows and head_dim 128 two per CU (VGPRs, LDS), four
+    // waves x 32 rows at head_dim 64 and one-wave shapes three.
+    const int64_t slots = 256 * ((p.variant == ffai::kWave4x2 || d->head_dim == 128) ? 2 : 3);
+    if (d->causal) {
+      // Causal, rank order longest first: when the longest item is well above a resident slot's
+      // share of the work, it bounds the launch; the items longer than half the longest go in 2
+      // pieces. Qwen2-VL-2B prefill (Hq 12, S 4096, D 128: 384 items of 2..64 tiles, the 192
+      // longest split): 76.4 us against 89.3 unsplit (same run; 108 before rank-order dispatch).
+      const int64_t nbh = (int64_t)d->batch * d->heads_q;
+      auto tiles_of = [&](int64_t qb) {  // keys any row of query block qb sees, in tiles
+        const int64_t kv = std::min<int64_t>(d->kv_len, std::max<int64_t>(0, d->q_offset + std::min<int64_t>((qb + 1) * bm, d->q_len)));
+        return (kv + ffai::kBlockN - 1) / ffai::kBlockN;
+      };
+      int64_t total = 0;
+      for (int64_t qb = 0; qb < p.n_qblk; ++qb) total += tiles_of(qb) * nbh;
+      const int64_t longest = tiles_of(p.n_qblk - 1);
+      if (longest >= 4 && longest * 5 > 6 * (total / slots)) {
+        int64_t n = 0;  // rank order: query blocks descending, all (batch, head) of each
+        for (int64_t qb = p.n_qblk - 1; qb >= 0 && 2 * tiles_of(qb) > longest; --qb) n += nbh;
+        if (n > 0) { want = 2; lo = 0; hi = n; optional = true; }
+      }
+    } else if (items > slots && n_tiles >= 8) {
+      // Non-causal: a last round of at most a quarter of the slots runs its items in 4 pieces.
+      // whisper-small (B8 H12 T1500: 576 items, 512 resident): 78.7 us against 85.5 with the
+      // last 64 items in 4 pieces (2: 79.4, 6: 103.6); whisper-large-v3 (1920 items, a last
+      // round of 384) runs best unsplit (210.3 us; its last 128 items in 2 pieces: 212.2).
+      const int64_t tail = items % slots;
+      if (tail > 0 && 4 * tail <= slots) {
+        want = 4; lo = items - tail; hi = items; optional = true;
+      }
+    }
   }
-  p.n_work = (int)(work * p.n_split);
-  p.ws_bytes = p.n_split > 1 ? ffai::kCounterBytes +
-                                   (size_t)bh * p.n_split * d->q_len * (d->head_dim + 2) * 4
-                             : 0;
+  // ffai_set_fwd_split_override forces the split items and their pieces.
+  const int o_items = g_split_items.load(std::memory_order_relaxed);
+  const int o_pieces = g_split_pieces.load(std::memory_order_relaxed);
+  if (o_items != 0 && o_pieces >= 1) {  // pieces 1: nothing split
+    want = o_pieces;
+    const int64_t n = o_items < 0 ? items : std::min<int64_t>(o_items, items);
+    // non-causal: the items dispatched last; causal: the longest, dispatched first
+    lo = d->causal ? 0 : items - n;
+    hi = d->causal ? n : items;
+  }
+  // a counter slot per split item; the partials addressed by 32-bit byte offsets
+  want = std::min<int64_t>({want, n_tiles, ffai::kMaxFwdSplits});
+  const int64_t want_bytes = (hi - lo) * want * bm * (d->head_dim + 2) * 4;
+  if (allow_split && want > 1 && hi > lo && hi - lo <= ffai::kCounterSlots &&
+      want_bytes < (int64_t(1) << 31) &&
+      !(optional && ffai::kCounterBytes + (size_t)want_bytes > max_ws)) {
+    p.n_split = (int)want;
+    p.tiles_per_split = (n_tiles + p.n_split - 1) / p.n_split;
+    p.split_lo = (int)lo;
+    p.split_hi = (int)hi;
+  }
+  const int64_t pieces = (int64_t)(p.split_hi - p.split_lo) * p.n_split;
+  p.n_work = (int)(items + pieces - (p.split_hi - p.split_lo));
+  // Dispatch. Causal: rank order (longest first) across all XCDs. Otherwise each section's works
+  // go to the XCDs in contiguous runs (one head's query blocks, one item's pieces share an L2);
+  // split items at the end of the grid form the second section, so that they are dealt to every
+  // XCD and dispatched after the whole items.
+  p.xcd_remap = !d->causal;
+  p.sec1_work = (p.split_hi > p.split_lo && p.split_lo > 0) ? p.split_lo : p.n_work;
+  const size_t part_bytes = (size_t)pieces * bm * (d->head_dim + 2) * 4;
+  p.ws_bytes = pieces > 0 ? ffai::kCounterBytes + part_bytes : 0;
   return p;
 }
 
@@ -330,7 +408,7 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
                        vec_of(v, ks, d->v_strides, need_kv) == need_kv &&
                        vec_of(out, os, d->o_strides, 4) == 4;
 
-  const Plan pl = make_plan(d, allow_split, aligned);
+  const Plan pl = make_plan(d, allow_split, aligned, use_scratch ? kScratchBytes : SIZE_MAX);
   if (use_scratch && pl.ws_bytes > kScratchBytes)
     return fail(FFAI_ERR_WORKSPACE,
                 "this shape needs " + std::to_string(pl.ws_bytes) +
@@ -387,8 +465,13 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   p.o_sb = d->o_strides[0]; p.o_sh = d->o_strides[1]; p.o_st = d->o_strides[2];
   p.B = d->batch; p.Hq = d->heads_q; p.Hkv = d->heads_kv; p.Tq = d->q_len; p.Tk = d->kv_len;
   p.causal = d->causal; p.q_offset = d->q_offset;
-  p.n_qblk = pl.n_qblk; p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split;
+  p.n_qblk = pl.n_qblk;
+  p.split_lo = pl.split_lo; p.split_hi = pl.split_hi; p.n_split = pl.n_split;
   p.n_work = pl.n_work;
+  p.sec1_work = pl.sec1_work;
+  p.sec1_wgs = (pl.sec1_work + 7) / 8 * 8;
+  p.xcd_remap = pl.xcd_remap ? 1 : 0;
+  p.counters = static_cast<int32_t*>(ws);
   p.aligned = aligned;
   {
     // the DMA path addresses a tile's rows by 32-bit byte offsets from the tile's first key
@@ -398,16 +481,8 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
             int64_t(ffai::kBlockN) * d->v_strides[2] * 2 < lim;
   }
   p.scale_log2 = d->scale * 1.4426950408889634f;
-  hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt, pl.variant, s);
+  const hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt, pl.variant, s);
   if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));
-  if (pl.n_split > 1) {
-    ffai::CombineParams c{};
-    c.ws = p.ws; c.o = out;
-    c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
-    c.B = p.B; c.Hq = p.Hq; c.Tq = p.Tq; c.n_split = p.n_split;
-    e = ffai::launch_combine(c, ot, d->head_dim, s);
-    if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("combine launch: ") + hipGetErrorString(e));
-  }
   return FFAI_OK;
 }
 
@@ -558,6 +633,19 @@ int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]) {
   return FFAI_OK;
 }
 
+int ffai_attn_plan_splits(const ffai_attn_desc* d, int32_t info[3]) {
+  if (!info) return fail(FFAI_ERR_INVALID, "null info pointer");
+  std::string why;
+  const int rc = check_desc(d, &why);
+  if (rc == FFAI_DECLINED) return fail(FFAI_DECLINED, "declined: " + why);
+  if (rc != FFAI_OK) return fail(rc, why);
+  const Plan p = make_plan(d, true, true);
+  info[0] = p.decode ? 0 : p.n_items;
+  info[1] = p.decode ? 0 : p.split_lo;
+  info[2] = p.decode ? 0 : p.split_hi;
+  return FFAI_OK;
+}
+
 int ffai_serves(const ffai_tensor* kt, const ffai_tensor* v) {
   if (!kt || !v || !kt->on_device || !v->on_device) return 0;
   if (kt->dims[0] != 1 || kt->dims[2] != kHD || v->dims[0] != 1 || v->dims[3] != kHD) return 0;
@@ -637,6 +725,16 @@ int ffai_get_decode_tiles_per_wg(void) { return decode_tiles_per_wg(); }
 
 void ffai_set_decode_tiles_per_wg(int n) {
   if (n >= 0) g_decode_tps.store(n, std::memory_order_relaxed);
+}
+
+void ffai_set_fwd_split_override(int items, int pieces) {
+  g_split_items.store(items, std::memory_order_relaxed);
+  g_split_pieces.store(pieces, std::memory_order_relaxed);
+}
+
+void ffai_get_fwd_split_override(int* items, int* pieces) {
+  if (items) *items = g_split_items.load(std::memory_order_relaxed);
+  if (pieces) *pieces = g_split_pieces.load(std::memory_order_relaxed);
 }
 
 void ffai_set_decode_min_keys(int n) {

@@ -27,8 +27,10 @@
 //     weight and sum finite in f32.
 //   * Workgroup ids are remapped so that all query blocks of one (batch, kv-head) run on the
 //     same XCD (the hardware deals workgroup i to XCD i % 8) and share that XCD's L2.
-//   * Few-query shapes (decode) split the keys over workgroups; partial (O, m, l) go to the
-//     workspace and combine_kernel merges them by log-sum-exp.
+//   * Items (batch, head, query block) may run as several pieces, each a contiguous key range:
+//     every item of a short grid, the last round's items of a long one, the longest items of a
+//     causal one. Pieces write partial (O, m, l) to the workspace and the item's last piece to
+//     finish merges them by log-sum-exp in the same launch.
 #pragma once
 
 #include "attn_common.cuh"
@@ -78,18 +80,38 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   __shared__ __attribute__((aligned(16))) LT k_lds[NBK * KBUF];
   __shared__ __attribute__((aligned(16))) LT v_lds[NBUF * VBUF];
 
-  // ---- which (batch, head, query block, key split) this workgroup computes
+  // ---- which work (an item, or one piece of a split item) this workgroup computes
   const int hw = blockIdx.x;
-  const int work = (hw & 7) * (int)(gridDim.x >> 3) + (hw >> 3);
-  if (work >= p.n_work) return;
-  int rest = work;
-  const int split = rest % p.n_split;
-  rest /= p.n_split;
-  int qb = rest % p.n_qblk;
-  rest /= p.n_qblk;
-  const int h = rest % p.Hq;
-  const int b = rest / p.Hq;
-  if (p.causal) qb = p.n_qblk - 1 - qb;  // longest rows first
+  int work;
+  if (hw < p.sec1_wgs) {
+    work = p.xcd_remap ? (hw & 7) * (p.sec1_wgs >> 3) + (hw >> 3) : hw;
+    if (work >= p.sec1_work) return;
+  } else {
+    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;  // n: a multiple of 8
+    work = p.sec1_work + (p.xcd_remap ? (x & 7) * (n >> 3) + (x >> 3) : x);
+    if (work >= p.n_work) return;
+  }
+  const int n_pieces = (p.split_hi - p.split_lo) * p.n_split;
+  int rank, split = -1;  // split: the piece of a split item, -1 for a whole item
+  if (work < p.split_lo) {
+    rank = work;
+  } else if (work < p.split_lo + n_pieces) {
+    rank = p.split_lo + (work - p.split_lo) / p.n_split;
+    split = (work - p.split_lo) % p.n_split;
+  } else {
+    rank = work - n_pieces + (p.split_hi - p.split_lo);
+  }
+  int qb, bh;
+  if (p.causal) {  // longest rows first: query block descending, then (batch, head)
+    const int nbh = p.B * p.Hq;
+    qb = p.n_qblk - 1 - rank / nbh;
+    bh = rank % nbh;
+  } else {
+    qb = rank % p.n_qblk;
+    bh = rank / p.n_qblk;
+  }
+  const int h = bh % p.Hq;
+  const int b = bh / p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
 
   const int tid = threadIdx.x;
@@ -106,8 +128,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   int kv_blk = kv_end;  // keys any row of this workgroup may see
   if (p.causal) kv_blk = min(kv_end, max(0, p.q_offset + min(qb * BM + BM, p.Tq)));
   const int n_tiles = (kv_blk + BN - 1) / BN;
-  const int t_begin = split * p.tiles_per_split;
-  const int t_end = min(n_tiles, t_begin + p.tiles_per_split);
+  const int tps = split < 0 ? n_tiles : (n_tiles + p.n_split - 1) / p.n_split;
+  const int t_begin = split < 0 ? 0 : split * tps;
+  const int t_end = min(n_tiles, t_begin + tps);
   const bool aligned = p.aligned != 0;
 
   const QS* qp = reinterpret_cast<const QS*>(p.q) + b * p.q_sb + h * p.q_sh;
@@ -839,82 +862,133 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   }
 
   // ---- epilogue: oacc[c][dt][4r + e] <-> d = 32dt + 8r + 4g + e of query q0 + 32c + n32
+  float l_tot[QW];
 #pragma unroll
-  for (int c = 0; c < QW; ++c) {
-    const float l_tot = partner_sum(l_run[c]);
-    const int qrow = q0 + 32 * c + n32;
-    if (qrow >= p.Tq) continue;
-    if (p.n_split == 1) {
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
-                          (int64_t)qrow * p.o_st;
+  for (int c = 0; c < QW; ++c) l_tot[c] = partner_sum(l_run[c]);
+  if (split >= 0) {
+    // A piece of a split item: publish this piece's partial (unnormalised O rows, and per row the
+    // reference max m in scaled log2 units and the weight sum l), count the piece, and let the
+    // item's last piece merge the others into its own registers by log-sum-exp.
+    const int S = p.n_split;
+    const int j = rank - p.split_lo;  // the item's counter and partial slot
+    const int64_t rows_all = (int64_t)(p.split_hi - p.split_lo) * S * BM;
+    const int64_t o_floats = rows_all * D;
+    // a buffer resource over exactly the partials (an access past them reads 0 / is dropped)
+    const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        p.ws, (short)0, (int)((o_floats + rows_all * 2) * 4), kBufferWord3);
+    const int64_t item_row0 = (int64_t)j * S * BM;  // row 0 of the item's piece 0
+    const int lrow0 = wave * 32 * QW + n32;         // this lane's row in a piece (column block 0)
+    // Device-scope (sc1) stores: each reaches the device's coherence point before it is
+    // acknowledged, so the last piece reads it on whichever XCD that piece runs.
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const f32x4 x = {oacc[c][dt][4 * r] * inv, oacc[c][dt][4 * r + 1] * inv,
-                           oacc[c][dt][4 * r + 2] * inv, oacc[c][dt][4 * r + 3] * inv};
-          if (aligned) st4<OUTT, true>(op + 32 * dt + 8 * r + 4 * g, x);
-          else st4<OUTT, false>(op + 32 * dt + 8 * r + 4 * g, x);
-        }
-    } else {
-      const int64_t prow = ((int64_t)(b * p.Hq + h) * p.n_split + split) * p.Tq + qrow;
-      float* wo = p.ws + prow * D;
+    for (int c = 0; c < QW; ++c) {
+      if (q0 + 32 * c + n32 >= p.Tq) continue;
+      const int64_t prow = item_row0 + (int64_t)split * BM + lrow0 + 32 * c;
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const f32x4 x = {oacc[c][dt][4 * r], oacc[c][dt][4 * r + 1], oacc[c][dt][4 * r + 2],
                            oacc[c][dt][4 * r + 3]};
-          *reinterpret_cast<f32x4*>(wo + 32 * dt + 8 * r + 4 * g) = x;
+          __builtin_amdgcn_raw_buffer_store_b128(
+              x, ws_rsrc, (int)((prow * D + 32 * dt + 8 * r + 4 * g) * 4), 0, kDeviceScope);
         }
-      if (g == 0) {
-        float* ml = p.ws + (int64_t)p.B * p.Hq * p.n_split * p.Tq * D + prow * 2;
-        *reinterpret_cast<f32x2*>(ml) = f32x2{m_s[c], l_tot};  // max in scaled log2 units
+      if (g == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(f32x2{m_s[c], l_tot[c]}, ws_rsrc,
+                                              (int)((o_floats + prow * 2) * 4), 0, kDeviceScope);
+    }
+    // Ordering: every thread waits until its stores are acknowledged (vmcnt(0); a device-scope
+    // store is acknowledged once visible at device scope), the barrier makes that true of the
+    // whole workgroup, and only then does one thread add 1 to the item's counter (device-scope
+    // atomic). The piece that reads S - 1 back is the item's last: every other piece's partial
+    // was visible before its increment, which precedes this one in the counter's order, and this
+    // workgroup's device-scope loads are issued after that increment returned. The last piece
+    // sets the counter back to 0 for the next launch (no piece ever waits for another).
+    // The flag lives in the tile buffers, which every wave has finished with at the barrier (a
+    // __shared__ int of its own would push head_dim 128's 80 KB past two workgroups per CU).
+    int* s_last = reinterpret_cast<int*>(k_lds);
+    vm_wait_all();
+    __syncthreads();
+    if (tid == 0) {
+      const int done =
+          __hip_atomic_fetch_add(p.counters + j, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = (done == S - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    // Merge all S pieces (this one's too, as stored) in piece order, so that the result does not
+    // depend on which piece finished last: KP pieces' loads in flight per round trip.
+    constexpr int KP = 2;
+#pragma unroll
+    for (int c = 0; c < QW; ++c) {
+      m_s[c] = kNegInf;
+      l_tot[c] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[c][dt][r] = 0.f;
+    }
+#pragma unroll 1
+    for (int s0 = 0; s0 < S; s0 += KP) {
+      f32x2 ml[KP][QW];
+      f32x4 xs[KP][QW][D / 32][4];
+#pragma unroll
+      for (int u = 0; u < KP; ++u) {
+        const int s = min(s0 + u, S - 1);  // clamped; a slot past the last piece counts as empty
+#pragma unroll
+        for (int c = 0; c < QW; ++c) {
+          const int64_t prow = item_row0 + (int64_t)s * BM + lrow0 + 32 * c;
+          ml[u][c] = __builtin_amdgcn_raw_buffer_load_b64(ws_rsrc, (int)((o_floats + prow * 2) * 4),
+                                                          0, kDeviceScope);
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              xs[u][c][dt][r] = __builtin_amdgcn_raw_buffer_load_b128(
+                  ws_rsrc, (int)((prow * D + 32 * dt + 8 * r + 4 * g) * 4), 0, kDeviceScope);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < KP; ++u) {
+        const bool real = s0 + u < S;  // wave-uniform
+#pragma unroll
+        for (int c = 0; c < QW; ++c) {
+          const float m = real ? ml[u][c][0] : kNegInf;
+          const float m_new = fmaxf(m_s[c], m);
+          const float mc = (m_new == kNegInf) ? 0.f : m_new;  // both empty: weights 0, not NaN
+          const float c_old = fast_exp2(m_s[c] - mc);          // 0 while m_s is -inf
+          const float c_new = fast_exp2(m - mc);               // 0 for an empty piece
+          l_tot[c] = l_tot[c] * c_old + (real ? ml[u][c][1] : 0.f) * c_new;
+#pragma unroll
+          for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                oacc[c][dt][4 * r + e] =
+                    oacc[c][dt][4 * r + e] * c_old + (real ? xs[u][c][dt][r][e] : 0.f) * c_new;
+          m_s[c] = m_new;
+        }
       }
     }
+    if (tid == 0) __hip_atomic_store(p.counters + j, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-// Merge split-key partials by log-sum-exp. D/4 lanes per (batch, head, query row), four elements
-// each, so a 256-thread workgroup merges 1024/D rows (one workgroup per row spent the launch on
-// dispatch: 30000 workgroups for one whisper-large-v3 window). Partial maxima are in scaled log2
-// units.
-template <int OUTT, int D>
-__global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
-  constexpr int LPR = D / 4, RPB = 256 / LPR;
-  const int rows = p.B * p.Hq * p.Tq;
-  const int row = blockIdx.x * RPB + threadIdx.x / LPR;
-  if (row >= rows) return;
-  const int c4 = threadIdx.x % LPR;  // this lane's 4 elements: 4 c4 .. 4 c4 + 3
-  const int t = row % p.Tq;
-  const int bh = row / p.Tq;
-  const int h = bh % p.Hq, b = bh / p.Hq;
-  const int64_t base = (int64_t)bh * p.n_split * p.Tq + t;  // partial row of split 0
-  const float* wo = p.ws + base * D + 4 * c4;
-  const float* ml = p.ws + (int64_t)p.B * p.Hq * p.n_split * p.Tq * D + base * 2;
-  const int64_t so = (int64_t)p.Tq * D, sml = (int64_t)p.Tq * 2;
-  float m = kNegInf;
-#pragma unroll 4
-  for (int s = 0; s < p.n_split; ++s) m = fmaxf(m, ml[s * sml]);
-  const float mu = (m == kNegInf) ? 0.f : m;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-#pragma unroll 4
-  for (int s = 0; s < p.n_split; ++s) {
-    const f32x2 ms = *reinterpret_cast<const f32x2*>(ml + s * sml);
-    const float w = fast_exp2(ms[0] - mu);  // 0 for an empty split (m = -inf)
-    l = __builtin_fmaf(w, ms[1], l);
-    acc += w * *reinterpret_cast<const f32x4*>(wo + s * so);
-  }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
-                      (int64_t)t * p.o_st + 4 * c4;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float x = acc[e] * inv;
-    if constexpr (OUTT == kF32) op[e] = x;
-    else op[e] = from_f32<OUTT>(x);
+  for (int c = 0; c < QW; ++c) {
+    const int qrow = q0 + 32 * c + n32;
+    if (qrow >= p.Tq) continue;
+    const float inv = l_tot[c] > 0.f ? 1.f / l_tot[c] : 0.f;
+    store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
+                        (int64_t)qrow * p.o_st;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const f32x4 x = {oacc[c][dt][4 * r] * inv, oacc[c][dt][4 * r + 1] * inv,
+                         oacc[c][dt][4 * r + 2] * inv, oacc[c][dt][4 * r + 3] * inv};
+        if (aligned) st4<OUTT, true>(op + 32 * dt + 8 * r + 4 * g, x);
+        else st4<OUTT, false>(op + 32 * dt + 8 * r + 4 * g, x);
+      }
   }
 }
 

@@ -15,7 +15,9 @@ struct FwdParams {
   const void* k;
   const void* v;
   void* o;
-  float* ws;              // split-key partials: [B][Hq][n_split][Tq][D] O then [..][2] (m, l)
+  float* ws;              // split partials: [split items][n_split][block_m rows][D] O, then
+                          // [..][block_m][2] (m, l)
+  int32_t* counters;      // one per split item (kCounterSlots): zero before the launch and after
   const int32_t* kv_lens; // device int32[B] or nullptr
   int64_t q_sb, q_sh, q_st;
   int64_t k_sb, k_sh, k_st;  // k_st: stride between key rows (rows layout) or d rows (K^T)
@@ -24,9 +26,19 @@ struct FwdParams {
   int32_t B, Hq, Hkv, Tq, Tk;
   int32_t causal, q_offset;
   int32_t n_qblk;            // ceil(Tq / block_m)
-  int32_t n_split;           // key splits per (b, h, q-block); 1 = no partials
-  int32_t tiles_per_split;   // key tiles (of 64) per split
-  int32_t n_work;            // B * Hq * n_qblk * n_split logical workgroups
+  // Items are the (batch, head, query block) triples, in rank order: head-major, or for a causal
+  // launch longest first (query block descending, then batch and head). Items of rank
+  // [split_lo, split_hi) run as n_split pieces (contiguous key ranges of ceil(tiles / n_split)
+  // tiles each); the item's last piece to finish merges the others' partials in the same launch.
+  int32_t split_lo, split_hi;
+  int32_t n_split;           // pieces per split item (1 when no item is split)
+  int32_t n_work;            // items + (split_hi - split_lo) * (n_split - 1): works in rank order
+  // Dispatch: works [0, sec1_work) take the first sec1_wgs workgroups (a multiple of 8), the
+  // rest the remaining ones. With xcd_remap each section deals its works to the 8 XCDs in
+  // contiguous runs (hardware workgroup i goes to XCD i % 8), so neighbouring works (one head's
+  // query blocks, one item's pieces) share an L2; without it works go in rank order.
+  int32_t sec1_work, sec1_wgs;
+  int32_t xcd_remap;
   int32_t aligned;           // every operand admits the kernels' vector loads and stores
   int32_t dma;               // 16-bit: whole tiles may go global -> LDS by DMA (aligned, and
                              // each lane's byte offset within a K or V tile fits 32 bits)
@@ -54,21 +66,16 @@ struct DecodeParams {
   int32_t n_work;           // B * Hkv * n_split
   float scale_log2;
 };
-// Workspace layout shared by every plan: kCounterBytes of split counters (decode units, one
-// int32 each; zero at rest) first, then the partials of whichever kernel the plan runs. The
-// counters keep that place whatever plan last used the workspace, so partials never overwrite
-// them and a workspace zeroed once stays usable by every plan.
+// Workspace layout shared by every plan: kCounterBytes of split counters (decode units or split
+// fwd items, one int32 each; zero at rest) first, then the partials of whichever kernel the plan
+// runs. The counters keep that place whatever plan last used the workspace, so partials never
+// overwrite them and a workspace zeroed once stays usable by every plan.
 constexpr int kCounterSlots = 1024;
 constexpr size_t kCounterBytes = kCounterSlots * sizeof(int32_t);
 // Key splits of one decode unit at most (the merge loops over them).
 constexpr int kMaxDecodeSplits = 64;
-
-struct CombineParams {
-  const float* ws;
-  void* o;
-  int64_t o_sb, o_sh, o_st;
-  int32_t B, Hq, Tq, n_split;
-};
+// Pieces of one split fwd item at most (its merge loops over them).
+constexpr int kMaxFwdSplits = 64;
 
 // Launchers; return hipSuccess or the launch error.
 // mode: kBF16 / kF16 (MFMA bf16/f16 kernel, q and kv the same 16-bit type) or kF32 (f32 MFMA
@@ -82,10 +89,9 @@ enum Variant : int {
 };
 inline int block_m_of(int variant) { return variant == kWave1 ? 32 : variant == kWave4 ? 128 : 256; }
 
+// The grid is sec1_wgs plus the second section's works rounded up to a multiple of 8.
 hipError_t launch_fwd(const FwdParams& p, int mode, int kv_dtype, int out_dtype, int head_dim,
                       bool k_transposed, int variant, hipStream_t stream);
-hipError_t launch_combine(const CombineParams& p, int out_dtype, int head_dim,
-                          hipStream_t stream);
 // Per-dtype instantiation units (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip).
 hipError_t launch_fwd_bf16(const FwdParams& p, int out_dtype, int d, bool kt, int variant,
                            hipStream_t s);

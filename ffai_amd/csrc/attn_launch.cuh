@@ -8,7 +8,8 @@ namespace {
 
 template <int MODE, int KVT, int OUTT, int D, bool KT, int NW, int QW>
 hipError_t launch_one(const FwdParams& p, hipStream_t s) {
-  const unsigned grid = (unsigned)((p.n_work + 7) / 8 * 8);  // whole XCD rounds
+  // two dispatch sections, each in whole XCD rounds
+  const unsigned grid = (unsigned)(p.sec1_wgs + (p.n_work - p.sec1_work + 7) / 8 * 8);
   // Head_dim 128, four waves: 80 KB of LDS and <= 256 VGPRs admit two workgroups per CU. A grid
   // of fewer than two per CU then piles pairs onto some CUs and leaves others idle; 16 KB of
   // unused dynamic LDS keeps such a grid at one per CU (Qwen2-VL prefill, 384 workgroups:

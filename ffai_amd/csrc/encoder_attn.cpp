@@ -7,13 +7,16 @@
 // over batch items (text_decoder.rs:1069-1076). Below, B is the windows of one pass.
 //
 // Workspace (compute dtype T = bf16 or f16; B batch, S seq, N n_state, H heads, hd = N / H):
+//   attention workspace, first and at least the split counters' size: the counters must stay at
+//                          the same place, untouched by anything else, for calls of any shape
+//                          through one workspace (zeroed once, left zero by every call)
 //   q      (B, S, N)     = x Wq^T + bq       read by the kernel as (B, H, S, hd), strides (S N, hd, N, 1)
 //   v      (B, S, N)     = x Wv^T + bv       likewise
 //   kt     (N, B S)      = Wk_scaled x^T over every window at once: element (b, h, j, s) at
 //                          (h hd + j) B S + b S + s, read by the kernel as K^T with strides
 //                          (S, hd B S, B S, 1) -- one plain GEMM, no batched GEMM
 //   merged (B, S, N)     attention output, the kernel writing the merged layout directly
-//   attention workspace, then hipBLASLt scratch
+//   hipBLASLt scratch
 // With packed weights (wqkv, bqkv) the first three regions hold instead
 //   qkv    (B, S, 3N)    = x Wqkv^T + bqkv in one GEMM: q, k and v of one frame side by side,
 //                          read by the kernel with strides (S 3N, hd, 3N, 1) and K as rows
@@ -217,7 +220,7 @@ int sizes_of(const ffai_encoder_attn_desc* d, Sizes* z) {
     if (rc != FFAI_OK) return rc;
     aw = std::max(aw, b);
   }
-  z->attn = align256(aw);
+  z->attn = align256(std::max(aw, ffai::kCounterBytes));
   z->gemm = kGemmScratch;
   z->total = z->q + z->kt + z->v + z->merged + z->attn + z->gemm;
   return FFAI_OK;
@@ -253,12 +256,12 @@ int run_pass(const ffai_encoder_attn_desc* d, const void* x, const ffai_encoder_
     return api_fail(FFAI_ERR_INVALID, "one pass holds at most 1500 rows");
   int rc = FFAI_OK;
   char* ws = static_cast<char*>(workspace);
-  void* q = ws;
-  void* kt = ws + z.q;
-  void* v = ws + z.q + z.kt;
-  void* merged = ws + z.q + z.kt + z.v;
-  void* attn_ws = ws + z.q + z.kt + z.v + z.merged;
-  void* scratch = ws + z.q + z.kt + z.v + z.merged + z.attn;
+  void* attn_ws = ws;
+  void* q = ws + z.attn;
+  void* kt = ws + z.attn + z.q;
+  void* v = ws + z.attn + z.q + z.kt;
+  void* merged = ws + z.attn + z.q + z.kt + z.v;
+  void* scratch = ws + z.attn + z.q + z.kt + z.v + z.merged;
   const hipDataType dt = d->dtype == FFAI_BF16 ? HIP_R_16BF : HIP_R_16F;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t BS = (int64_t)d->batch * d->seq, N = d->n_state;

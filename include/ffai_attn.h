@@ -130,6 +130,13 @@ size_t ffai_attn_noalloc_scratch_bytes(void);
  * ffai_attn_workspace_bytes. */
 int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]);
 
+/* Diagnostic, no counterpart in the reference: which work items of the fused kernel's plan for
+ * `d` run as key-split pieces. Items are the (batch, head, query block) triples in dispatch rank
+ * (head-major; for a causal launch longest first); info[0]: items, info[1], info[2]: the split
+ * ranks [info[1], info[2]) (empty when nothing is split), each in info[2] of plan_info's pieces.
+ * Zeros for a decode plan. Returns as ffai_attn_plan_info. */
+int ffai_attn_plan_splits(const ffai_attn_desc* d, int32_t info[3]);
+
 /* ------------------------------------------------------------------------------------------
  * Mirrors of the reference's public functions.
  * ---------------------------------------------------------------------------------------- */
@@ -183,6 +190,15 @@ void ffai_set_decode_min_keys(int n);
  * how a decode call splits its keys over workgroups, never its result beyond f32 rounding. */
 int ffai_get_decode_tiles_per_wg(void);
 void ffai_set_decode_tiles_per_wg(int n);
+
+/* Tuning and test hook, no counterpart in the reference: force which items of the fused
+ * kernel run as key-split pieces. items > 0: that many items (the last ones dispatched of a
+ * non-causal launch, the longest ones of a causal launch), each in `pieces` pieces (1: no item
+ * is split); items < 0: every item; items == 0 or pieces < 1: the planner's choice (the default). The
+ * workspace a descriptor needs follows the setting. It changes how a call splits its keys,
+ * never its result beyond f32 rounding. */
+void ffai_set_fwd_split_override(int items, int pieces);
+void ffai_get_fwd_split_override(int* items, int* pieces);
 
 /* Human-readable description of the last error on the calling thread ("" if none). */
 const char* ffai_attn_last_error(void);

@@ -9,10 +9,12 @@ float64 closed form. Bars: 1e-4 max-abs for f32, 2e-2 for bf16.
 Workloads:
 * whisper-tiny encoder, B1 H6 T1500 D64, f32 (four-wave blocks, keys split);
 * whisper-small encoder, B8 H12 T1500 D64, K x 2, in f32 (one workgroup per 128 rows, no key
-  split: the f32 kernel's direct epilogue) and bf16 (four waves x 64 rows);
+  split: the f32 kernel's direct epilogue) and bf16 (four waves x 64 rows, the last round's
+  items in key pieces);
 * whisper-large-v3 encoder, B16 H20 T1500 D64, bf16 (one layer of the headline run);
 * Qwen2-VL-2B-shape causal prefill, Hq12 Hkv2 D128 S4096, bf16, Q and K rotated per position
-  by random 2-D rotations of dimension pairs (norm preserving), as rotary embedding leaves them;
+  by random 2-D rotations of dimension pairs (norm preserving), as rotary embedding leaves them
+  (longest query blocks in two key pieces);
 * the beam-5 whisper-medium decode step: self-attention over ragged bf16 caches (lengths
   U{1..448}) and cross-attention of 5 beams over 1500 shared frames.
 """
@@ -82,10 +84,14 @@ def test_whisper_tiny_f32_full_size(gpu):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_whisper_small_full_size(gpu, dtype):
     """B8 H12 T1500 with K x 2. f32: 1152 workgroups of 128 rows, keys whole (the direct store
-    of the f32 kernel's epilogue); bf16: four waves x 64 rows, keys whole."""
+    of the f32 kernel's epilogue); bf16: four waves x 64 rows, 576 items of which the last 64
+    (the round past the 512 resident workgroups) run in 4 key pieces merged in the launch."""
     q, kt, v = _encoder_case(2, 8, 12, 1500, 64, dtype, k_mult=2.0)
-    shape = "wave4" if dtype == torch.float32 else "wave4x2"
-    _run_encoder(gpu, q, kt, v, dtype, dtype, {"kernel": "fwd", "shape": shape, "splits": 1})
+    if dtype == torch.float32:
+        expect = {"kernel": "fwd", "shape": "wave4", "splits": 1}
+    else:
+        expect = {"kernel": "fwd", "shape": "wave4x2", "splits": 4, "split_items": (512, 576)}
+    _run_encoder(gpu, q, kt, v, dtype, dtype, expect)
 
 
 def test_whisper_large_v3_full_size(gpu):
@@ -125,7 +131,10 @@ def test_qwen2_vl_causal_prefill_full_size(gpu):
     out = torch.empty(1, 12, s, d, dtype=bf, device=gpu)
     plan = fa.plan(qd, kd, vd, out, scale=scale, causal=True)
     print("plan", plan)
-    assert plan["kernel"] == "fwd" and plan["shape"] == "wave4" and plan["splits"] == 1
+    # 384 items (12 heads x 32 query blocks of 128 rows) dispatched longest first; the 192
+    # longest (more than half the longest's keys) in 2 pieces merged in the launch
+    assert plan["kernel"] == "fwd" and plan["shape"] == "wave4" and plan["splits"] == 2
+    assert plan["split_items"] == (0, 192)
     assert fa.attention(qd, kd, vd, scale=scale, causal=True, out=out) is not None
     got = out.float().cpu().numpy()
     want = oracle.attend_general(q, k, v, k_transposed=False, scale=scale, causal=True,

@@ -1,0 +1,188 @@
+"""GPU parity of the fused kernel's key-split pieces: items that run as several workgroups over
+contiguous key ranges, merged by the item's last piece in the same launch.
+
+The split layout is forced with ffai_set_fwd_split_override so that every arrangement runs at
+sizes the oracle finishes in seconds: the tail of a non-causal grid (a second dispatch section
+after the whole items), the longest items of a causal grid, every item, ragged items whose later
+pieces hold no keys. Each case checks the output against the oracle (1e-4 f32, 2e-2 16-bit),
+the plan's split ranks, and that the counters at the workspace's start are zero again.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ffai_amd import _lib as L
+from ffai_amd import flash_attn as fa
+from tests.helpers import TOL_BF16, TOL_F32, max_abs, randn, round_bf16, round_f16
+
+pytestmark = pytest.mark.gpu
+
+COUNTER_BYTES = 4096
+
+
+@pytest.fixture
+def split_override():
+    prev = L.get_fwd_split_override()
+    yield L.set_fwd_split_override
+    L.set_fwd_split_override(*prev)
+
+
+def _dev(x, dtype, device):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device=device, dtype=dtype)
+
+
+def _run(q, k, v, *, out_dtype, **kw):
+    """One call with an explicit zeroed workspace; returns (out, plan, workspace)."""
+    out = torch.empty(q.shape[0], q.shape[1], q.shape[2], v.shape[3], dtype=out_dtype,
+                      device=q.device)
+    n = fa.workspace_bytes(q, k, v, out, **kw)
+    ws = torch.zeros(max(n, 1), dtype=torch.uint8, device=q.device)
+    plan = fa.plan(q, k, v, out, **kw)
+    res = fa.attention(q, k, v, out=out, workspace=ws, **kw)
+    assert res is not None
+    torch.cuda.synchronize()
+    return out, plan, ws
+
+
+def _counters_zero(ws):
+    return int(ws[:COUNTER_BYTES].count_nonzero().item()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k_transposed", [True, False])
+def test_tail_items_in_pieces(gpu, split_override, dtype, k_transposed):
+    """Non-causal, four waves x 32 rows: the last 37 of 90 items in 4 pieces each, dispatched as
+    a second section after the 53 whole items."""
+    rng = np.random.default_rng(37)
+    b, h, t, d = 3, 5, 700, 64
+    rnd = round_bf16 if dtype == torch.bfloat16 else round_f16
+    q = rnd(randn(rng, (b, h, t, d)))
+    k = rnd(randn(rng, (b, h, d, t) if k_transposed else (b, h, t, d)))
+    v = rnd(randn(rng, (b, h, t, d)))
+    split_override(37, 4)
+    out, plan, ws = _run(_dev(q, dtype, gpu), _dev(k, dtype, gpu), _dev(v, dtype, gpu),
+                         out_dtype=torch.float32, k_transposed=k_transposed, scale=0.125)
+    assert plan["kernel"] == "fwd" and plan["shape"] == "wave4"
+    assert plan["items"] == 90 and plan["split_items"] == (53, 90) and plan["splits"] == 4
+    want = oracle.attend_general(q, k, v, k_transposed=k_transposed, scale=0.125)
+    err = max_abs(out.cpu().numpy(), want)
+    print(f"tail pieces {dtype} kt={k_transposed}: {err:.3e}")
+    assert err < TOL_BF16
+    assert _counters_zero(ws)
+
+
+def test_tail_items_in_pieces_two_column_blocks(gpu, split_override):
+    """The encoder's launch shape (four waves x 64 rows, K transposed): 512 items, the last 100
+    in 3 pieces."""
+    rng = np.random.default_rng(512)
+    b, h, t, d = 16, 16, 512, 64
+    q = round_bf16(randn(rng, (b, h, t, d)))
+    kt = round_bf16(randn(rng, (b, h, d, t)))
+    v = round_bf16(randn(rng, (b, h, t, d)))
+    split_override(100, 3)
+    out, plan, ws = _run(_dev(q, torch.bfloat16, gpu), _dev(kt, torch.bfloat16, gpu),
+                         _dev(v, torch.bfloat16, gpu), out_dtype=torch.bfloat16,
+                         k_transposed=True, scale=0.125)
+    assert plan["shape"] == "wave4x2" and plan["items"] == 512
+    assert plan["split_items"] == (412, 512) and plan["splits"] == 3
+    want = oracle.attend_general(q, kt, v, k_transposed=True, scale=0.125)
+    err = max_abs(out.float().cpu().numpy(), want)
+    print(f"tail pieces 4x2: {err:.3e}")
+    assert err < TOL_BF16
+    assert _counters_zero(ws)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_longest_causal_items_in_pieces(gpu, split_override, d):
+    """Causal GQA (Hq 4, Hkv 2, S 700): the 5 longest items in 3 pieces, dispatched first."""
+    rng = np.random.default_rng(700 + d)
+    b, hq, hkv, s = 1, 4, 2, 700
+    q = round_bf16(randn(rng, (b, hq, s, d)))
+    k = round_bf16(randn(rng, (b, hkv, s, d)))
+    v = round_bf16(randn(rng, (b, hkv, s, d)))
+    split_override(5, 3)
+    out, plan, ws = _run(_dev(q, torch.bfloat16, gpu), _dev(k, torch.bfloat16, gpu),
+                         _dev(v, torch.bfloat16, gpu), out_dtype=torch.float32,
+                         scale=d ** -0.5, causal=True)
+    assert plan["split_items"] == (0, 5) and plan["splits"] == 3
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=d ** -0.5, causal=True)
+    err = max_abs(out.cpu().numpy(), want)
+    print(f"causal longest pieces d{d}: {err:.3e}")
+    assert err < TOL_BF16
+    assert _counters_zero(ws)
+
+
+@pytest.mark.parametrize("items,pieces", [(-1, 7), (3, 2)])
+def test_f32_items_in_pieces(gpu, split_override, items, pieces):
+    """The f32 kernel (whisper-tiny heads) with every item in 7 pieces, and with the last 3
+    items in 2."""
+    rng = np.random.default_rng(600 + pieces)
+    h, t, d = 6, 600, 64
+    q = randn(rng, (1, h, t, d)) * np.float32(0.125)
+    kt, v = randn(rng, (1, h, d, t)), randn(rng, (1, h, t, d))
+    split_override(items, pieces)
+    out, plan, ws = _run(_dev(q, torch.float32, gpu), _dev(kt, torch.float32, gpu),
+                         _dev(v, torch.float32, gpu), out_dtype=torch.float32,
+                         k_transposed=True, scale=1.0)
+    n = plan["items"]
+    assert plan["split_items"] == ((0, n) if items < 0 else (n - items, n))
+    assert plan["splits"] == pieces
+    want = oracle.attend_general(q, kt, v, k_transposed=True, scale=1.0)
+    err = max_abs(out.cpu().numpy(), want)
+    print(f"f32 pieces {items}x{pieces}: {err:.3e}")
+    assert err < TOL_F32
+    assert _counters_zero(ws)
+
+
+def test_ragged_items_with_empty_pieces(gpu, split_override):
+    """Per-batch key counts 300, 1, 65, 200 with every item in 5 pieces: the short items' later
+    pieces hold no keys and must count as empty in the merge."""
+    rng = np.random.default_rng(5)
+    b, h, t, tk, d = 4, 2, 300, 300, 64
+    lens = np.array([300, 1, 65, 200], np.int32)
+    q = round_bf16(randn(rng, (b, h, t, d)))
+    k = round_bf16(randn(rng, (b, h, tk, d)))
+    v = round_bf16(randn(rng, (b, h, tk, d)))
+    split_override(-1, 5)
+    out, plan, ws = _run(_dev(q, torch.bfloat16, gpu), _dev(k, torch.bfloat16, gpu),
+                         _dev(v, torch.bfloat16, gpu), out_dtype=torch.float32, scale=0.125,
+                         kv_lens=torch.from_numpy(lens).to(gpu))
+    assert plan["splits"] == 5
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=0.125, kv_lens=lens)
+    err = max_abs(out.cpu().numpy(), want)
+    print(f"ragged empty pieces: {err:.3e}")
+    assert err < TOL_BF16
+    assert _counters_zero(ws)
+
+
+def test_one_workspace_across_split_layouts(gpu, split_override):
+    """A workspace zeroed once serves calls of different split layouts in a row (every call
+    leaves its counters zero); each result matches the unsplit call."""
+    rng = np.random.default_rng(11)
+    b, h, t, d = 2, 4, 900, 64
+    q = _dev(round_bf16(randn(rng, (b, h, t, d))), torch.bfloat16, gpu)
+    k = _dev(round_bf16(randn(rng, (b, h, t, d))), torch.bfloat16, gpu)
+    v = _dev(round_bf16(randn(rng, (b, h, t, d))), torch.bfloat16, gpu)
+    want = oracle.attend_general(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                 v.float().cpu().numpy(), k_transposed=False, scale=0.125)
+    sizes = []
+    for items, pieces in [(-1, 8), (10, 3), (20, 2), (-1, 4)]:
+        split_override(items, pieces)
+        sizes.append(fa.workspace_bytes(q, k, v, torch.empty_like(q, dtype=torch.float32),
+                                        scale=0.125))
+    ws = torch.zeros(max(sizes), dtype=torch.uint8, device=gpu)
+    for items, pieces in [(-1, 8), (10, 3), (20, 2), (-1, 4)]:
+        split_override(items, pieces)
+        out = torch.empty(b, h, t, d, dtype=torch.float32, device=gpu)
+        assert fa.attention(q, k, v, scale=0.125, out=out, workspace=ws) is not None
+        torch.cuda.synchronize()
+        err = max_abs(out.cpu().numpy(), want)
+        print(f"layout {items}x{pieces}: {err:.3e}")
+        assert err < TOL_BF16
+        assert _counters_zero(ws)

@@ -73,7 +73,7 @@ def test_decode_splits_twice(gpu):
 
 @pytest.mark.gpu
 def test_encoder_splits_twice(gpu):
-    """whisper-tiny f32 encoder (6 heads x 1500 rows: four-wave blocks with the keys split, ~36
+    """whisper-tiny f32 encoder (6 heads x 1500 rows: four-wave blocks with the keys split, ~7
     MB of partials), then a smaller f32 one (2 heads x 300 rows), then a 16-bit prompt-step
     shape (one-wave blocks, split keys, 228 rows x 16 heads over 1500 frames)."""
     lib = L.load()
@@ -95,6 +95,29 @@ def test_encoder_splits_twice(gpu):
 
 
 @pytest.mark.gpu
+def test_balance_splits_twice(gpu):
+    """The splits made for balance only: whisper-small bf16 (B8 H12 T1500, its last 64 items in
+    4 key pieces, ~17 MB of partials), then the smaller Qwen2-VL-2B causal prefill (Hq12 Hkv2
+    S4096 D128, its 192 longest items in 2 pieces, ~26 MB)."""
+    lib = L.load()
+    g = torch.Generator(device=gpu).manual_seed(73)
+    q = _rand((8, 12, 1500, 64), torch.bfloat16, gpu, g)
+    kt = _rand((8, 12, 64, 1500), torch.bfloat16, gpu, g, 2.0)
+    v = _rand((8, 12, 1500, 64), torch.bfloat16, gpu, g)
+    o_ws, o_na, nbytes = _both(lib, q, kt, v, k_transposed=True, scale=0.125,
+                               out_dtype=torch.bfloat16)
+    assert nbytes > 0
+    _check(o_ws, o_na, "whisper-small tail pieces")
+    q = _rand((1, 12, 4096, 128), torch.bfloat16, gpu, g)
+    k = _rand((1, 2, 4096, 128), torch.bfloat16, gpu, g)
+    v = _rand((1, 2, 4096, 128), torch.bfloat16, gpu, g)
+    o_ws, o_na, nbytes = _both(lib, q, k, v, scale=128 ** -0.5, causal=True,
+                               out_dtype=torch.bfloat16)
+    assert nbytes > 0
+    _check(o_ws, o_na, "causal prefill longest pieces")
+
+
+@pytest.mark.gpu
 def test_unsplit_shape_needs_no_scratch(gpu):
     """A shape without partials (4 x 20 heads x 1500 rows, bf16) runs the same through both."""
     lib = L.load()
@@ -109,21 +132,28 @@ def test_unsplit_shape_needs_no_scratch(gpu):
 
 
 def test_refuses_partials_above_the_scratch():
-    """A plan whose partials exceed the scratch is refused before any GPU call (head_dim 128,
-    one head, 32640 rows: three key splits of 255 workgroups, ~51 MB of partials)."""
+    """A plan whose partials exceed the scratch is refused before any GPU call: four
+    whisper-large-v3 windows (480 items of 256 rows) forced into 8 key pieces each, ~259 MB of
+    partials."""
     lib = L.load()
     cap = lib.ffai_attn_noalloc_scratch_bytes()
     assert cap == 48 << 20
     d = L.AttnDesc()
-    lib.ffai_attn_desc_init(ctypes.byref(d), L.BF16, L.BF16, L.BF16, 1, 1, 1, 32640, 32640, 128,
-                            L.K_ROWS)
-    n = ctypes.c_size_t(0)
-    assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == L.FFAI_OK
-    assert n.value > cap
-    fake = 0x10000
-    rc = lib.ffai_attn_fwd_noalloc(ctypes.byref(d), fake, fake, fake, fake, None)
-    assert rc == L.FFAI_ERR_WORKSPACE
-    assert "allocation-free" in L.last_error()
-    # a descriptor the path declines is declined, as by ffai_attn_fwd
-    d.head_dim = 96
-    assert lib.ffai_attn_fwd_noalloc(ctypes.byref(d), fake, fake, fake, fake, None) == L.FFAI_DECLINED
+    lib.ffai_attn_desc_init(ctypes.byref(d), L.BF16, L.BF16, L.BF16, 4, 20, 20, 1500, 1500, 64,
+                            L.K_TRANSPOSED)
+    prev = L.get_fwd_split_override()
+    L.set_fwd_split_override(-1, 8)
+    try:
+        n = ctypes.c_size_t(0)
+        assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == L.FFAI_OK
+        assert n.value > cap
+        fake = 0x10000
+        rc = lib.ffai_attn_fwd_noalloc(ctypes.byref(d), fake, fake, fake, fake, None)
+        assert rc == L.FFAI_ERR_WORKSPACE
+        assert "allocation-free" in L.last_error()
+        # a descriptor the path declines is declined, as by ffai_attn_fwd
+        d.head_dim = 96
+        assert lib.ffai_attn_fwd_noalloc(ctypes.byref(d), fake, fake, fake, fake,
+                                         None) == L.FFAI_DECLINED
+    finally:
+        L.set_fwd_split_override(*prev)
