@@ -18,8 +18,8 @@ the CPU oracle (the reference's algorithm restated in C++/AVX2) timed on this ho
 bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras] [--eager]
-                       [--layers L] [--legs decode,state,block,gemv,tiny,small,prefill,floor | none
-                       | copy]
+                       [--layers L]
+                       [--legs decode,state,block,gemv,tiny,small,prefill,floor,pipes | none | copy]
 """
 
 from __future__ import annotations
@@ -48,9 +48,10 @@ def parse():
     ap.add_argument("--eager", action="store_true",
                     help="decode leg without HIP graphs (for counter collection)")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill,floor",
+    ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill,floor,pipes",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "state, block, gemv, tiny, small, prefill, floor, or 'none'; 'copy' alone "
+                         "state, block, gemv, tiny, small, prefill, floor, pipes, or 'none'; "
+                         "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
 
@@ -206,6 +207,41 @@ def floor_bench(torch, steps=50, launches=24, nbytes=6_175_744, sets=3, workgrou
         us = timed(read)
         res["read_us"][str(wg)] = us
         res["read_gbps"][str(wg)] = nbytes / (us * 1e-6) / 1e9
+    return res
+
+
+def pipes_bench(torch, iters=4096, waves_per_simd=(1, 2, 4)):
+    """Pipe rates behind the fused kernel's per-tile budget (ffai_probe_pipes): per iteration
+    and per SIMD, the time of 4 bf16 32x32x16 MFMAs, of 8 v_exp_f32, of 8 FMAs, and of the
+    MFMAs with 8 (16) exp and 8 (16) FMA spread between them, at 1, 2 and 4 waves per SIMD.
+    `mfma_tflops` is the chip rate the MFMA-only loop reaches; cycles are at 2.4 GHz."""
+    import ctypes
+    from ffai_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    out = torch.empty(256 * 256 * max(waves_per_simd), dtype=torch.float32, device=dev)
+    kinds = ("mfma4", "exp8", "fma8", "mfma4+exp8+fma8", "mfma4+exp16+fma16")
+    res = {"iters": iters, "cycles_at_2p4ghz_per_iter_per_simd": {}, "mfma_tflops": {}}
+    for w in waves_per_simd:
+        wgs = 256 * w
+        row = {}
+        for k, name in enumerate(kinds):
+            def launch():
+                _lib.check(lib.ffai_probe_pipes(k, wgs, iters, out.data_ptr(),
+                                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+            launch()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch()
+            e1.record()
+            torch.cuda.synchronize()
+            ns = e0.elapsed_time(e1) * 1e6 / (iters * w)  # per iteration per SIMD
+            row[name] = round(ns * 2.4, 1)
+            if k == 0:
+                res["mfma_tflops"][str(w)] = round(4 * 32768 * 1024 * w * iters / (e0.elapsed_time(e1) * 1e-3) / 1e12, 1)
+        res["cycles_at_2p4ghz_per_iter_per_simd"][str(w)] = row
     return res
 
 
@@ -812,6 +848,12 @@ def main():
         log(f"launch floor: empty {fl['empty_us']:.2f} us, 6 MB read "
             + ", ".join(f"{k} WGs {v:.2f} us" for k, v in fl["read_us"].items()))
         extras["launch_floor"] = fl
+    if "pipes" in legs:
+        log("pipe rates: MFMA, v_exp_f32, FMA and mixes ...")
+        pr = pipes_bench(torch)
+        log(f"pipes: MFMA-only {pr['mfma_tflops']} TFLOP/s by waves per SIMD; cycles per "
+            f"iteration per SIMD at 2.4 GHz {pr['cycles_at_2p4ghz_per_iter_per_simd']}")
+        extras["pipe_rates"] = pr
     cpu = None
     if not args.skip_cpu:
         log("cpu baselines (oracle restating the reference's kernel) ...")

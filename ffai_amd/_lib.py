@@ -142,7 +142,8 @@ def load():
                                          ctypes.c_size_t, vp]
     L.ffai_probe_empty.argtypes = [ctypes.c_int, vp]
     L.ffai_probe_read.argtypes = [vp, sz, vp, ctypes.c_int, vp]
-    for name in ("ffai_probe_empty", "ffai_probe_read", "ffai_attn_serves",
+    L.ffai_probe_pipes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+    for name in ("ffai_probe_empty", "ffai_probe_read", "ffai_probe_pipes", "ffai_attn_serves",
                  "ffai_attn_workspace_bytes", "ffai_attn_fwd",
                  "ffai_attn_plan_info", "ffai_attn_plan_splits", "ffai_attn_fwd_noalloc",
                  "ffai_serves",

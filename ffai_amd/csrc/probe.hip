@@ -1,5 +1,6 @@
-// Launch-floor probes (include/ffai_probe.h): an empty kernel, and a bare streaming read, so
-// that the per-launch floor under the decode kernels can be measured beside them.
+// Probes (include/ffai_probe.h): an empty kernel and a bare streaming read, so that the
+// per-launch floor under the decode kernels can be measured beside them; and pipe-rate loops
+// (MFMA, v_exp_f32, FMA, and their mixes) behind the fused kernel's per-tile cycle budget.
 #include "../../include/ffai_probe.h"
 
 #include <hip/hip_runtime.h>
@@ -43,6 +44,44 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const u32x4* src, int64
   }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Per iteration: NM bf16 32x32x16 MFMAs on NM independent accumulators, NE v_exp_f32 and NF FMAs
+// on 8 independent chains (exp2(-e) and e * 0.5 + 0.25 stay bounded), the VALU share spread
+// evenly between the MFMAs. Every thread writes one float so that nothing is dead code.
+template <int NM, int NE, int NF>
+__global__ __launch_bounds__(256) void probe_pipes_kernel(int iters, float seed, float* out) {
+  bf16x8 x;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (__bf16)(seed + 0.01f * i + 1e-4f * threadIdx.x);
+  f32x16 acc[NM > 0 ? NM : 1] = {};
+  float e[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) e[j] = seed * (j + 1) * 1e-3f + threadIdx.x * 1e-6f;
+  constexpr int G = NM > 0 ? NM : 1;  // VALU groups per iteration
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int m = 0; m < G; ++m) {
+      if constexpr (NM > 0) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, x, acc[m], 0, 0, 0);
+#pragma unroll
+      for (int j = m * NE / G; j < (m + 1) * NE / G; ++j)
+        e[j % 8] = __builtin_amdgcn_exp2f(-e[j % 8]);
+#pragma unroll
+      for (int j = m * NF / G; j < (m + 1) * NF / G; ++j)
+        e[j % 8] = __builtin_fmaf(e[j % 8], 0.5f, 0.25f);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int m = 0; m < G; ++m)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += acc[m][i];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += e[j];
+  out[(int64_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -63,6 +102,22 @@ int ffai_probe_read(const void* src, size_t bytes, float* out, int workgroups, v
   hipLaunchKernelGGL(probe_read_kernel, dim3((unsigned)workgroups), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
                      (int64_t)(bytes / 16), out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FFAI_OK : ffai::api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
+}
+
+int ffai_probe_pipes(int kind, int workgroups, int iters, float* out, void* stream) {
+  if (!out || workgroups < 1 || iters < 1 || kind < 0 || kind > 4)
+    return ffai::api_fail(FFAI_ERR_INVALID, "kind 0..4, workgroups >= 1, iters >= 1, out set");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 g((unsigned)workgroups), b(256);
+  switch (kind) {
+    case 0: hipLaunchKernelGGL((probe_pipes_kernel<4, 0, 0>), g, b, 0, s, iters, 1.f, out); break;
+    case 1: hipLaunchKernelGGL((probe_pipes_kernel<0, 8, 0>), g, b, 0, s, iters, 1.f, out); break;
+    case 2: hipLaunchKernelGGL((probe_pipes_kernel<0, 0, 8>), g, b, 0, s, iters, 1.f, out); break;
+    case 3: hipLaunchKernelGGL((probe_pipes_kernel<4, 8, 8>), g, b, 0, s, iters, 1.f, out); break;
+    default: hipLaunchKernelGGL((probe_pipes_kernel<4, 16, 16>), g, b, 0, s, iters, 1.f, out); break;
+  }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FFAI_OK : ffai::api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
 }
