@@ -263,14 +263,18 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // than CUs take up to three, so that about every CU holds a piece: whisper-tiny (6 heads, 72
   // items) bf16 20.7 us in 3 pieces against 27.0 whole, f32 55.1 against 71.8 in 2 and 87.8 in
   // 15; a whisper-large-v3 window (20 heads, 240 items) runs best whole: 27.7 us against 31.2 in
-  // 2 and 39.7 in 3. One-wave grids (prompt steps) keep about 512 workgroups (cross-attention of
-  // 228 tokens, 128 items: 19.3 us in 4 pieces against 22.3 in 2 and 26.2 in 8), at most 8 pieces
-  // an item in f32.
+  // 2 and 39.7 in 3. f32 four-wave grids up to 1024 items aim at ~4096 waves (300 items: 183 us
+  // in 4 pieces against 236 whole, 197 in 2, 211 in 8). One-wave grids (prompt steps, f32 and
+  // misaligned decode) keep about 512 workgroups: the cross-attention of 228 tokens, 128 items,
+  // 19.3 us in 4 pieces against 22.3 in 2 and 26.2 in 8; f32 decode over 1500 keys, 6 heads:
+  // 25.9 us in 24 pieces, 32.7 in 8, 193 whole; 80 items: 55.8 in 7, 73.9 in 4, 86.8 in 24.
   int64_t want = 1;
   if (p.variant == ffai::kWave1) {
-    if (items < 512) want = std::min<int64_t>(f32 ? 8 : ffai::kMaxFwdSplits, (512 + items - 1) / items);
+    if (items < 512) want = std::min<int64_t>(f32 ? 24 : ffai::kMaxFwdSplits, (512 + items - 1) / items);
   } else if (items < 256) {
     want = std::max<int64_t>(1, std::min<int64_t>(3, 256 / items));
+  } else if (f32 && items < 1024) {
+    want = (4096 + 4 * items - 1) / (4 * items);
   }
   // FFAI_ATTN_SPLITS (> 0) forces the pieces of every item: a tuning knob.
   static const int forced_splits = [] {
