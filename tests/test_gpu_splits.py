@@ -10,8 +10,6 @@ the plan's split ranks, and that the counters at the workspace's start are zero 
 
 from __future__ import annotations
 
-import ctypes
-
 import numpy as np
 import pytest
 import torch
@@ -163,7 +161,7 @@ def test_ragged_items_with_empty_pieces(gpu, split_override):
 
 def test_one_workspace_across_split_layouts(gpu, split_override):
     """A workspace zeroed once serves calls of different split layouts in a row (every call
-    leaves its counters zero); each result matches the unsplit call."""
+    leaves its counters zero); each result matches the oracle."""
     rng = np.random.default_rng(11)
     b, h, t, d = 2, 4, 900, 64
     q = _dev(round_bf16(randn(rng, (b, h, t, d))), torch.bfloat16, gpu)
@@ -186,3 +184,54 @@ def test_one_workspace_across_split_layouts(gpu, split_override):
         print(f"layout {items}x{pieces}: {err:.3e}")
         assert err < TOL_BF16
         assert _counters_zero(ws)
+
+
+def test_pieces_in_graph_replays(gpu, split_override):
+    """A launch with split items captured in a HIP graph: every replay (with eager work and
+    synchronisation between replays, new inputs copied in) equals the eager call on the same
+    inputs bit for bit, and leaves the counters zero. Past the counters the workspace starts as
+    garbage (0xFF): partials are written before they are read."""
+    rng = np.random.default_rng(77)
+    b, h, t, d = 2, 3, 700, 64
+    split_override(9, 3)
+    q = torch.empty(b, h, t, d, dtype=torch.bfloat16, device=gpu)
+    k = torch.empty(b, h, d, t, dtype=torch.bfloat16, device=gpu)
+    v = torch.empty(b, h, t, d, dtype=torch.bfloat16, device=gpu)
+    out = torch.empty(b, h, t, d, dtype=torch.float32, device=gpu)
+    args = dict(k_transposed=True, scale=0.125)
+    plan = fa.plan(q, k, v, out, **args)
+    assert plan["splits"] == 3 and plan["split_items"][1] - plan["split_items"][0] == 9
+    nbytes = fa.workspace_bytes(q, k, v, out, **args)
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=gpu)
+    ws[:COUNTER_BYTES].zero_()
+    inputs = [tuple(_dev(round_bf16(randn(rng, x.shape)), torch.bfloat16, gpu) for x in (q, k, v))
+              for _ in range(3)]
+
+    def call():
+        fa.attention(q, k, v, out=out, workspace=ws, **args)
+
+    eager = []
+    for qi, ki, vi in inputs:
+        q.copy_(qi); k.copy_(ki); v.copy_(vi)
+        call()
+        torch.cuda.synchronize()
+        eager.append(out.clone())
+        assert _counters_zero(ws)
+    want = oracle.attend_general(inputs[0][0].float().cpu().numpy(),
+                                 inputs[0][1].float().cpu().numpy(),
+                                 inputs[0][2].float().cpu().numpy(), k_transposed=True,
+                                 scale=0.125)
+    assert max_abs(eager[0].cpu().numpy(), want) < TOL_BF16
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        call()
+    for i in range(6):
+        qi, ki, vi = inputs[i % 3]
+        q.copy_(qi); k.copy_(ki); v.copy_(vi)
+        out.fill_(float(i + 1))     # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[i % 3]), f"replay {i} differs"
+        assert _counters_zero(ws), f"replay {i} left a counter set"
