@@ -868,7 +868,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   if (split >= 0) {
     // A piece of a split item: publish this piece's partial (unnormalised O rows, and per row the
     // reference max m in scaled log2 units and the weight sum l), count the piece, and let the
-    // item's last piece merge the others into its own registers by log-sum-exp.
+    // item's last piece merge every piece's partial, in piece order, by log-sum-exp.
     const int S = p.n_split;
     const int j = rank - p.split_lo;  // the item's counter and partial slot
     const int64_t rows_all = (int64_t)(p.split_hi - p.split_lo) * S * BM;
