@@ -333,3 +333,69 @@ def test_gemv_entry_points_reject_bad_arguments(lib):
     assert n.value >= 5 * 1024 + 5 * 4
     assert lib.ffai_vocab_int8_logits(FAKE, FAKE, FAKE, 51865, 1024, 32, FAKE, 5, 1024, FAKE,
                                       51865, FAKE, 1, None) == L.FFAI_ERR_WORKSPACE
+
+
+# ---------------------------------------------------------------------------------------------
+# launch plans of the benchmarked workloads (host logic only)
+# ---------------------------------------------------------------------------------------------
+
+def _plan(lib, *args, causal=0):
+    d = desc(lib, *args)
+    d.causal = causal
+    info = (ctypes.c_int32 * 5)()
+    assert lib.ffai_attn_plan_info(ctypes.byref(d), info) == L.FFAI_OK
+    sp = (ctypes.c_int32 * 3)()
+    assert lib.ffai_attn_plan_splits(ctypes.byref(d), sp) == L.FFAI_OK
+    return list(info), list(sp)
+
+
+@pytest.mark.parametrize("args,causal,info,splits", [
+    # whisper-large-v3 encoder: 1920 items of 256 rows, none split (a last round of 384 of 512)
+    ((L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED), 0,
+     [0, 2, 1, 24, 1920], [1920, 0, 0]),
+    # whisper-small: 576 items on 512 resident, the last 64 in 4 pieces
+    ((L.BF16, L.BF16, L.BF16, 8, 12, 12, 1500, 1500, 64, L.K_TRANSPOSED), 0,
+     [0, 2, 4, 6, 768], [576, 512, 576]),
+    # whisper-tiny f32: 72 items in 3 pieces
+    ((L.F32, L.F32, L.F32, 1, 6, 6, 1500, 1500, 64, L.K_TRANSPOSED), 0,
+     [0, 1, 3, 8, 216], [72, 0, 72]),
+    # Qwen2-VL-2B prefill: 384 items longest first, the 192 longest in 2 pieces
+    ((L.BF16, L.BF16, L.BF16, 1, 12, 2, 4096, 4096, 128, L.K_ROWS), 1,
+     [0, 1, 2, 32, 576], [384, 0, 192]),
+    # the same at batch 4: the longest item is below a slot's share, nothing split
+    ((L.BF16, L.BF16, L.BF16, 4, 12, 2, 4096, 4096, 128, L.K_ROWS), 1,
+     [0, 1, 1, 64, 1536], [1536, 0, 0]),
+    # a whisper-large-v3 window (encoder block): 240 items, whole
+    ((L.BF16, L.BF16, L.BF16, 1, 20, 20, 1500, 1500, 64, L.K_ROWS), 0,
+     [0, 1, 1, 24, 240], [240, 0, 0]),
+    # prompt step cross-attention: 228 tokens x 16 heads, one-wave items in 4 pieces
+    ((L.BF16, L.BF16, L.F32, 1, 16, 16, 228, 1500, 64, L.K_TRANSPOSED), 0,
+     [0, 0, 4, 6, 512], [128, 0, 128]),
+    # beam-5 cross-attention: the decode kernel, 8 pieces of 3 tiles per head (128 workgroups)
+    ((L.BF16, L.BF16, L.F32, 1, 16, 16, 5, 1500, 64, L.K_TRANSPOSED), 0,
+     [1, 4, 8, 3, 128], [0, 0, 0]),
+])
+def test_plans_of_the_benchmarked_workloads(lib, args, causal, info, splits):
+    got_info, got_splits = _plan(lib, *args, causal=causal)
+    assert (got_info, got_splits) == (info, splits)
+
+
+def test_split_override_and_its_workspace(lib):
+    """The override forces the layout and the workspace follows it; (0, 0) restores the plan."""
+    prev = L.get_fwd_split_override()
+    try:
+        args = (L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED)
+        L.set_fwd_split_override(100, 3)
+        info, sp = _plan(lib, *args)
+        assert info[2] == 3 and sp == [1920, 1820, 1920] and info[4] == 1820 + 300
+        d = desc(lib, *args)
+        n = ctypes.c_size_t(0)
+        assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == L.FFAI_OK
+        assert n.value == 4096 + 100 * 3 * 256 * 66 * 4   # counters + partials of 300 pieces
+        L.set_fwd_split_override(-1, 1)                     # nothing split
+        assert _plan(lib, *args)[1] == [1920, 0, 0]
+        L.set_fwd_split_override(0, 0)
+        assert _plan(lib, *args)[1] == [1920, 0, 0]
+        assert L.get_fwd_split_override() == (0, 0)
+    finally:
+        L.set_fwd_split_override(*prev)
