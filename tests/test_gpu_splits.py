@@ -235,3 +235,56 @@ def test_pieces_in_graph_replays(gpu, split_override):
         torch.cuda.synchronize()
         assert torch.equal(out, eager[i % 3]), f"replay {i} differs"
         assert _counters_zero(ws), f"replay {i} left a counter set"
+
+
+def _seeded_cases(n=24, seed=2026):
+    """Small random shapes over every launch layout the planner and the override can make."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        d = int(rng.choice([64, 128]))
+        dtype = ["bf16", "f16", "f32"][i % 3] if d == 64 else ["bf16", "f16"][i % 2]
+        hkv = int(rng.integers(1, 4))
+        hq = hkv * int(rng.integers(1, 4)) if dtype != "f32" else hkv
+        b = int(rng.integers(1, 4))
+        causal = bool(rng.integers(0, 2)) and dtype != "f32"
+        tk = int(rng.integers(40, 700))
+        tq = int(rng.integers(1, 400)) if not causal else int(rng.integers(1, tk + 1))
+        q_offset = tk - tq if causal else 0
+        ragged = bool(rng.integers(0, 2))
+        items = int(rng.choice([0, -1, 1, 3, 7]))
+        pieces = int(rng.integers(2, 6))
+        k_transposed = bool(rng.integers(0, 2))
+        cases.append((i, b, hq, hkv, tq, tk, d, dtype, causal, q_offset, ragged, items, pieces,
+                      k_transposed))
+    return cases
+
+
+@pytest.mark.parametrize("case", _seeded_cases(), ids=lambda c: f"case{c[0]}")
+def test_seeded_layouts_against_the_oracle(gpu, split_override, case):
+    """Seeded random shapes (batch, grouped heads, head_dim 64/128, 16-bit and f32, causal with
+    the queries at the end of the keys, ragged key counts including empty ones, K rows or K
+    transposed) under the planner's layout or a forced one (the last / longest 1, 3 or 7 items or
+    every item in 2-5 pieces), against the oracle. Query counts up to 32 take the decode kernel."""
+    i, b, hq, hkv, tq, tk, d, dtype, causal, q_offset, ragged, items, pieces, k_transposed = case
+    rng = np.random.default_rng(1000 + i)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    rnd = {"bf16": round_bf16, "f16": round_f16, "f32": lambda x: x}[dtype]
+    q = rnd(randn(rng, (b, hq, tq, d)))
+    k = rnd(randn(rng, (b, hkv, d, tk) if k_transposed else (b, hkv, tk, d)))
+    v = rnd(randn(rng, (b, hkv, tk, d)))
+    lens = rng.integers(0, tk + 1, size=b).astype(np.int32) if ragged else None
+    if items:
+        split_override(items, pieces)
+    scale = d ** -0.5
+    kw = dict(scale=scale, causal=causal, q_offset=q_offset, k_transposed=k_transposed)
+    if lens is not None:
+        kw["kv_lens"] = torch.from_numpy(lens).to(gpu)
+    out, plan, ws = _run(_dev(q, tdt, gpu), _dev(k, tdt, gpu), _dev(v, tdt, gpu),
+                         out_dtype=torch.float32, **kw)
+    want = oracle.attend_general(q, k, v, k_transposed=k_transposed, scale=scale, causal=causal,
+                                 q_offset=q_offset, kv_lens=lens)
+    err = max_abs(out.cpu().numpy(), want)
+    print(f"case {case}: plan {plan}, err {err:.3e}")
+    assert err < (TOL_F32 if dtype == "f32" else TOL_BF16)
+    assert _counters_zero(ws)
