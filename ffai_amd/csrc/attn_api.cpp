@@ -259,12 +259,14 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   p.n_split = 1;
   p.tiles_per_split = n_tiles;
   p.split_lo = p.split_hi = 0;
-  // Short grids run every item in pieces (merged in the launch). Four-wave grids of fewer items
-  // than CUs take up to three, so that about every CU holds a piece: whisper-tiny (6 heads, 72
-  // items) bf16 20.7 us in 3 pieces against 27.0 whole, f32 55.1 against 71.8 in 2 and 87.8 in
-  // 15; a whisper-large-v3 window (20 heads, 240 items) runs best whole: 27.7 us against 31.2 in
-  // 2 and 39.7 in 3. f32 four-wave grids up to 1024 items aim at ~4096 waves (300 items: 183 us
-  // in 4 pieces against 236 whole, 197 in 2, 211 in 8). One-wave grids (prompt steps, f32 and
+  // Short grids run every item in pieces (merged in the launch). 16-bit four-wave grids of fewer
+  // items than CUs take up to three, so that about every CU holds a piece: whisper-tiny (6
+  // heads, 72 items) bf16 17.1 us in 3 pieces against 26.3 whole (6: 17.0); a whisper-large-v3
+  // window (20 heads, 240 items) runs whole: 27.4 us against 26.6 in 2 and 27.4 in 3. f32
+  // four-wave grids (two workgroups per CU) of fewer items than CUs fill the 512 slots:
+  // whisper-tiny f32 50.5 us in 6 pieces against 56.4 in 3, 66.2 in 4 (288 works: a second
+  // round) and 77.9 in 2; up to 1024 items they aim at ~4096 waves (300 items: 183 us in 4
+  // pieces against 236 whole, 197 in 2, 211 in 8). One-wave grids (prompt steps, f32 and
   // misaligned decode) keep about 512 workgroups: the cross-attention of 228 tokens, 128 items,
   // 19.3 us in 4 pieces against 22.3 in 2 and 26.2 in 8; f32 decode over 1500 keys, 6 heads:
   // 25.9 us in 24 pieces, 32.7 in 8, 193 whole; 80 items: 55.8 in 7, 73.9 in 4, 86.8 in 24.
@@ -272,7 +274,7 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   if (p.variant == ffai::kWave1) {
     if (items < 512) want = std::min<int64_t>(f32 ? 24 : ffai::kMaxFwdSplits, (512 + items - 1) / items);
   } else if (items < 256) {
-    want = std::max<int64_t>(1, std::min<int64_t>(3, 256 / items));
+    want = f32 ? 512 / items : std::max<int64_t>(1, std::min<int64_t>(3, 256 / items));
   } else if (f32 && items < 1024) {
     want = (4096 + 4 * items - 1) / (4 * items);
   }
@@ -321,7 +323,8 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // ffai_set_fwd_split_override forces the split items and their pieces.
   const int o_items = g_split_items.load(std::memory_order_relaxed);
   const int o_pieces = g_split_pieces.load(std::memory_order_relaxed);
-  if (o_items != 0 && o_pieces >= 1) {  // pieces 1: nothing split
+  const bool overridden = o_items != 0 && o_pieces >= 1;
+  if (overridden) {  // pieces 1: nothing split
     want = o_pieces;
     const int64_t n = o_items < 0 ? items : std::min<int64_t>(o_items, items);
     // non-causal: the items dispatched last; causal: the longest, dispatched first
@@ -330,6 +333,9 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   }
   // a counter slot per split item; the partials addressed by 32-bit byte offsets
   want = std::min<int64_t>({want, n_tiles, ffai::kMaxFwdSplits});
+  // no piece without tiles: as many pieces as ceil(tiles / n)-tile ranges cover the keys (a
+  // forced layout is kept as given)
+  if (want > 1 && !overridden) want = (n_tiles + (n_tiles + want - 1) / want - 1) / ((n_tiles + want - 1) / want);
   const int64_t want_bytes = (hi - lo) * want * bm * (d->head_dim + 2) * 4;
   if (allow_split && want > 1 && hi > lo && hi - lo <= ffai::kCounterSlots &&
       want_bytes < (int64_t(1) << 31) &&

@@ -876,14 +876,21 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     // a buffer resource over exactly the partials (an access past them reads 0 / is dropped)
     const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         p.ws, (short)0, (int)((o_floats + rows_all * 2) * 4), kBufferWord3);
-    const int64_t item_row0 = (int64_t)j * S * BM;  // row 0 of the item's piece 0
-    const int lrow0 = wave * 32 * QW + n32;         // this lane's row in a piece (column block 0)
+    // Partials are laid out lane-major, in the accumulators' register order: for piece
+    // (item j, piece s), wave w and column block c, register group (dt, r) of all 64 lanes is
+    // 1 KB of consecutive f32x4, so that every store and load instruction moves whole cache
+    // lines; (m, l) follows per (piece, wave, c) as 32 f32x2 by query column. Only the kernel
+    // itself reads them, and the last piece's thread (w, lane) merges exactly what thread
+    // (w, lane) of every piece wrote.
+    auto cw_of = [&](int s, int c) {  // (piece, wave, column block) index
+      return ((int64_t)(j * S + s) * NW + wave) * QW + c;
+    };
     // Device-scope (sc1) stores: each reaches the device's coherence point before it is
     // acknowledged, so the last piece reads it on whichever XCD that piece runs.
 #pragma unroll
     for (int c = 0; c < QW; ++c) {
       if (q0 + 32 * c + n32 >= p.Tq) continue;
-      const int64_t prow = item_row0 + (int64_t)split * BM + lrow0 + 32 * c;
+      const int64_t cw = cw_of(split, c);
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -891,11 +898,13 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
           const f32x4 x = {oacc[c][dt][4 * r], oacc[c][dt][4 * r + 1], oacc[c][dt][4 * r + 2],
                            oacc[c][dt][4 * r + 3]};
           __builtin_amdgcn_raw_buffer_store_b128(
-              x, ws_rsrc, (int)((prow * D + 32 * dt + 8 * r + 4 * g) * 4), 0, kDeviceScope);
+              x, ws_rsrc, (int)((((cw * (D / 32) + dt) * 4 + r) * 64 + lane) * 16), 0,
+              kDeviceScope);
         }
       if (g == 0)
         __builtin_amdgcn_raw_buffer_store_b64(f32x2{m_s[c], l_tot[c]}, ws_rsrc,
-                                              (int)((o_floats + prow * 2) * 4), 0, kDeviceScope);
+                                              (int)(o_floats * 4 + (cw * 32 + n32) * 8), 0,
+                                              kDeviceScope);
     }
     // Ordering: every thread waits until its stores are acknowledged (vmcnt(0); a device-scope
     // store is acknowledged once visible at device scope), the barrier makes that true of the
@@ -937,15 +946,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
         const int s = min(s0 + u, S - 1);  // clamped; a slot past the last piece counts as empty
 #pragma unroll
         for (int c = 0; c < QW; ++c) {
-          const int64_t prow = item_row0 + (int64_t)s * BM + lrow0 + 32 * c;
-          ml[u][c] = __builtin_amdgcn_raw_buffer_load_b64(ws_rsrc, (int)((o_floats + prow * 2) * 4),
-                                                          0, kDeviceScope);
+          const int64_t cw = cw_of(s, c);
+          ml[u][c] = __builtin_amdgcn_raw_buffer_load_b64(
+              ws_rsrc, (int)(o_floats * 4 + (cw * 32 + n32) * 8), 0, kDeviceScope);
 #pragma unroll
           for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               xs[u][c][dt][r] = __builtin_amdgcn_raw_buffer_load_b128(
-                  ws_rsrc, (int)((prow * D + 32 * dt + 8 * r + 4 * g) * 4), 0, kDeviceScope);
+                  ws_rsrc, (int)((((cw * (D / 32) + dt) * 4 + r) * 64 + lane) * 16), 0,
+                  kDeviceScope);
         }
       }
 #pragma unroll

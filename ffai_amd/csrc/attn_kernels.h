@@ -15,8 +15,9 @@ struct FwdParams {
   const void* k;
   const void* v;
   void* o;
-  float* ws;              // split partials: [split items][n_split][block_m rows][D] O, then
-                          // [..][block_m][2] (m, l)
+  float* ws;              // split partials, lane-major: [split items][n_split][waves][column
+                          // blocks][D / 32][4][64 lanes] f32x4 O in accumulator order, then
+                          // [..][waves][column blocks][32 query columns] (m, l)
   int32_t* counters;      // one per split item (kCounterSlots): zero before the launch and after
   const int32_t* kv_lens; // device int32[B] or nullptr
   int64_t q_sb, q_sh, q_st;

@@ -356,9 +356,9 @@ def _plan(lib, *args, causal=0):
     # whisper-small: 576 items on 512 resident, the last 64 in 4 pieces
     ((L.BF16, L.BF16, L.BF16, 8, 12, 12, 1500, 1500, 64, L.K_TRANSPOSED), 0,
      [0, 2, 4, 6, 768], [576, 512, 576]),
-    # whisper-tiny f32: 72 items in 3 pieces
+    # whisper-tiny f32: 72 items in 6 pieces (512 resident two-per-CU slots)
     ((L.F32, L.F32, L.F32, 1, 6, 6, 1500, 1500, 64, L.K_TRANSPOSED), 0,
-     [0, 1, 3, 8, 216], [72, 0, 72]),
+     [0, 1, 6, 4, 432], [72, 0, 72]),
     # Qwen2-VL-2B prefill: 384 items longest first, the 192 longest in 2 pieces
     ((L.BF16, L.BF16, L.BF16, 1, 12, 2, 4096, 4096, 128, L.K_ROWS), 1,
      [0, 1, 2, 32, 576], [384, 0, 192]),
