@@ -295,7 +295,8 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
       // Causal, rank order longest first: when the longest item is well above a resident slot's
       // share of the work, it bounds the launch; the items longer than half the longest go in 2
       // pieces. Qwen2-VL-2B prefill (Hq 12, S 4096, D 128: 384 items of 2..64 tiles, the 192
-      // longest split): 76.4 us against 89.3 unsplit (same run; 108 before rank-order dispatch).
+      // longest split): 72.5 us against 89.3 unsplit (same run; 108 before rank-order dispatch;
+      // 144 / 288 items 81.8 / 76.3, 3 pieces 96.0).
       const int64_t nbh = (int64_t)d->batch * d->heads_q;
       auto tiles_of = [&](int64_t qb) {  // keys any row of query block qb sees, in tiles
         const int64_t kv = std::min<int64_t>(d->kv_len, std::max<int64_t>(0, d->q_offset + std::min<int64_t>((qb + 1) * bm, d->q_len)));
@@ -311,9 +312,10 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
       }
     } else if (items > slots && n_tiles >= 8) {
       // Non-causal: a last round of at most a quarter of the slots runs its items in 4 pieces.
-      // whisper-small (B8 H12 T1500: 576 items, 512 resident): 78.7 us against 85.5 with the
-      // last 64 items in 4 pieces (2: 79.4, 6: 103.6); whisper-large-v3 (1920 items, a last
-      // round of 384) runs best unsplit (210.3 us; its last 128 items in 2 pieces: 212.2).
+      // whisper-small (B8 H12 T1500: 576 items, 512 resident): 75.2 us with the last 64 items
+      // in 4 pieces against 88.0 unsplit (2: 78.1, 6: 87.5); whisper-large-v3 (1920 items, a
+      // last round of 384) stays unsplit (219.9 us; its last 128 items in 2 pieces 212.4,
+      // within the spread of the rounds).
       const int64_t tail = items % slots;
       if (tail > 0 && 4 * tail <= slots) {
         want = 4; lo = items - tail; hi = items; optional = true;
