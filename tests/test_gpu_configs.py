@@ -78,7 +78,7 @@ def _run_encoder(gpu, q, kt, v, dtype, out_dtype, expect_plan):
 def test_whisper_tiny_f32_full_size(gpu):
     q, kt, v = _encoder_case(1, 1, 6, 1500, 64, torch.float32)
     _run_encoder(gpu, q, kt, v, torch.float32, torch.float32,
-                 {"kernel": "fwd", "shape": "wave4"})
+                 {"kernel": "fwd", "shape": "wave4", "splits": 6, "split_items": (0, 72)})
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
