@@ -420,6 +420,51 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
 
     us_state = timed(False)
     us_full = timed(True)
+    # the step's self-attention q/k/v projections with the appends: per layer the GEMV of the
+    # packed (3n, n) f16 weights and the append of its k and v rows, against one all-layer
+    # length advance and per layer the fused projection that writes the rows itself
+    from ffai_amd.gemv import F16Gemv
+    n = H * D
+    wqkv = [F16Gemv(torch.randn(3 * n, n, generator=gd, device=dev) / n ** 0.5)
+            for _ in range(layers)]
+    xq = torch.randn(beams, n, generator=gd, device=dev)
+    yq = torch.empty(beams, 3 * n, device=dev)
+    qo = torch.empty(beams, n, device=dev)
+
+    def proj_step(fused):
+        c = caches[0]
+        if fused:
+            c.advance(1)
+        for l in range(layers):
+            if fused:
+                wqkv[l].qkv_into_cache(xq, qo, c.layer(l))
+            else:
+                wqkv[l](xq, out=yq)
+                c.layer(l).append(yq[:, None, n:2 * n], yq[:, None, 2 * n:])
+
+    def timed_proj(fused):
+        caches[0].lens.fill_(start_len)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            proj_step(fused)
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            gr.replay()
+        stream = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            gr.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        final = int(caches[0].lens[0, 0])
+        assert final == start_len + total, (final, start_len, total)
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    us_proj_append = timed_proj(False)
+    us_proj_fused = timed_proj(True)
     # algorithmic bytes of the state work per step (lengths after the append, averaged over
     # the timed steps): append reads the f32 rows and writes bf16; the reorder reads and
     # writes every beam's valid prefix of K and V
@@ -492,6 +537,8 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
         "prompt_step_tflops": prompt_flop / (us_prompt * 1e-6) / 1e12,
         "prompt_tokens": P,
         "launches_per_step": layers + 1,
+        "qkv_and_append_us_per_step": us_proj_append,
+        "qkv_into_cache_us_per_step": us_proj_fused,
     }
 
 
@@ -801,7 +848,9 @@ def main():
         st = decode_state_bench(torch, fa, 100, 10)
         log(f"decode state: {st['state_us_per_step']:.1f} us/step ({st['state_gbps']:.0f} GB/s), "
             f"full step {st['full_step_us']:.1f} us, cross build {st['cross_build_us_per_window']:.1f} us, "
-            f"prompt step {st['prompt_step_us']:.1f} us ({st['prompt_step_tflops']:.1f} TFLOP/s)")
+            f"prompt step {st['prompt_step_us']:.1f} us ({st['prompt_step_tflops']:.1f} TFLOP/s), "
+            f"q/k/v + append {st['qkv_and_append_us_per_step']:.1f} us, fused "
+            f"{st['qkv_into_cache_us_per_step']:.1f} us")
         extras["decode_state_beam5"] = st
     if "block" in legs:
         log("encoder block: whisper-large-v3 projections + attention + out-projection ...")

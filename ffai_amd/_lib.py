@@ -131,11 +131,13 @@ def load():
     i32, i64 = ctypes.c_int32, ctypes.c_int64
     L.ffai_kv_append.argtypes = [cp, vp, vp, i32, i32, i64, i64, vp]
     L.ffai_kv_gather.argtypes = [cp, cp, vp, i32, i64, i64, vp]
+    L.ffai_kv_advance.argtypes = [cp, i32, i32, i64, vp]
     L.ffai_cross_kv_build.argtypes = [vp, vp, i32, i32, i32, i32, i64, vp, vp, i32, i32, vp]
     ed, ew = ctypes.POINTER(EncoderAttnDesc), ctypes.POINTER(EncoderAttnWeights)
     L.ffai_encoder_attn_workspace_bytes.argtypes = [ed, ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_encoder_attn_fwd.argtypes = [ed, vp, ew, vp, vp, ctypes.c_size_t, vp]
     L.ffai_gemv_f16.argtypes = [vp, i32, i32, vp, i32, i64, vp, i64, vp]
+    L.ffai_gemv_f16_qkv_cache.argtypes = [vp, vp, i32, vp, i32, i64, vp, i64, cp, vp]
     L.ffai_vocab_int8_quantize.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp]
     L.ffai_vocab_int8_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_vocab_int8_logits.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, i64, vp,
@@ -149,6 +151,7 @@ def load():
                  "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
+                 "ffai_kv_advance", "ffai_gemv_f16_qkv_cache",
                  "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",
                  "ffai_encoder_attn_fwd", "ffai_gemv_f16", "ffai_vocab_int8_quantize",
                  "ffai_vocab_int8_workspace_bytes", "ffai_vocab_int8_logits"):

@@ -42,18 +42,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 // multiplies them with every beam's x, read straight from global memory (the few KB of x stay
 // in L2; staging them in LDS behind a barrier put a second dependent round trip in front of the
 // weight loads), then the wave reduces each beam's sum.
+// Lane partial sums of output row `wr` with every beam's x (the wave sums them afterwards).
 template <int R>
-__global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restrict__ w,
-                                                       int out_dim, int in_dim,
-                                                       const float* __restrict__ x, int rows,
-                                                       int64_t xs, float* __restrict__ y,
-                                                       int64_t ys) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int o = blockIdx.x * 4 + wave;
-  if (o >= out_dim) return;
-  const uint16_t* wr = w + (int64_t)o * in_dim;
+__device__ __forceinline__ void gemv_row(const uint16_t* __restrict__ wr, int in_dim,
+                                         const float* __restrict__ x, int rows, int64_t xs,
+                                         int lane, float (&acc)[R]) {
   const int chunks = in_dim / 8;
-  float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
   constexpr int kBatch = 4;  // weight chunks in flight per lane
@@ -88,10 +82,74 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restric
       }
     }
   }
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restrict__ w,
+                                                       int out_dim, int in_dim,
+                                                       const float* __restrict__ x, int rows,
+                                                       int64_t xs, float* __restrict__ y,
+                                                       int64_t ys) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int o = blockIdx.x * 4 + wave;
+  if (o >= out_dim) return;
+  float acc[R];
+  gemv_row<R>(w + (int64_t)o * in_dim, in_dim, x, rows, xs, lane, acc);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float v = wave_sum(acc[r]);
     if (lane == r && r < rows) y[r * ys + o] = v;
+  }
+}
+
+// The self-attention q/k/v projection of a decode step with the new K/V rows written straight
+// into the layer's cache: weights packed (q; k; v), n = heads * head_dim outputs each. Output o
+// of beam r is the GEMV sum plus bias[o] (a separate f32 add, as the reference adds the bias
+// after the product); q goes to row r of `q`, k and v to position lens[r] - 1 of slot r, head
+// o / head_dim, converted to the cache type by round-to-nearest-even. The step's length advance
+// (ffai_kv_advance) runs before the layer, so lens[r] - 1 is the position it opened.
+struct QkvCacheParams {
+  const float* bias;  // 3n, or null
+  float* q;
+  int64_t qs;         // q row stride
+  void* ck;
+  void* cv;
+  const int32_t* lens;
+  int64_t cs, ch, cp;  // cache slot, head, position strides (elements)
+  int32_t n, head_dim, capacity;
+};
+
+template <int R, int CDT>
+__global__ __launch_bounds__(256) void gemv_f16_qkv_kernel(const uint16_t* __restrict__ w,
+                                                           int in_dim,
+                                                           const float* __restrict__ x, int rows,
+                                                           int64_t xs, QkvCacheParams p) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int o = blockIdx.x * 4 + wave;
+  if (o >= 3 * p.n) return;
+  float acc[R];
+  gemv_row<R>(w + (int64_t)o * in_dim, in_dim, x, rows, xs, lane, acc);
+  const int part = o / p.n;  // 0: q, 1: k, 2: v
+  const int oo = o - part * p.n;
+  const int h = oo / p.head_dim, d = oo - h * p.head_dim;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float v = wave_sum(acc[r]);
+    if (p.bias) v = v + p.bias[o];
+    if (lane == r && r < rows) {
+      if (part == 0) {
+        p.q[r * p.qs + oo] = v;
+      } else {
+        // a length outside [1, capacity] is clamped; 0 (no advance) writes nothing
+        const int pos = min(max(p.lens[r], 0), p.capacity) - 1;
+        if (pos >= 0) {
+          store_t<CDT>* c = reinterpret_cast<store_t<CDT>*>(part == 1 ? p.ck : p.cv) +
+                            (int64_t)r * p.cs + (int64_t)h * p.ch + (int64_t)pos * p.cp + d;
+          if constexpr (CDT == kF32) *c = v;
+          else *c = from_f32<CDT>(v);
+        }
+      }
+    }
   }
 }
 
@@ -101,6 +159,22 @@ hipError_t launch_gemv_any(const uint16_t* w, int out_dim, int in_dim, const flo
   const unsigned grid = (unsigned)((out_dim + 3) / 4);
   hipLaunchKernelGGL((gemv_f16_kernel<R>), dim3(grid), dim3(256), 0, st, w, out_dim,
                      in_dim, x, rows, xs, y, ys);
+  return hipGetLastError();
+}
+
+template <int R>
+hipError_t launch_qkv_cache(const uint16_t* w, int in_dim, const float* x, int rows, int64_t xs,
+                            const QkvCacheParams& p, int cdt, hipStream_t st) {
+  const unsigned grid = (unsigned)((3 * p.n + 3) / 4);
+  if (cdt == kF32)
+    hipLaunchKernelGGL((gemv_f16_qkv_kernel<R, kF32>), dim3(grid), dim3(256), 0, st, w, in_dim, x,
+                       rows, xs, p);
+  else if (cdt == kF16)
+    hipLaunchKernelGGL((gemv_f16_qkv_kernel<R, kF16>), dim3(grid), dim3(256), 0, st, w, in_dim, x,
+                       rows, xs, p);
+  else
+    hipLaunchKernelGGL((gemv_f16_qkv_kernel<R, kBF16>), dim3(grid), dim3(256), 0, st, w, in_dim,
+                       x, rows, xs, p);
   return hipGetLastError();
 }
 
@@ -267,6 +341,56 @@ int ffai_gemv_f16(const void* w, int32_t out_dim, int32_t in_dim, const float* x
     case 7: e = launch_gemv_any<7>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
     case 8: e = launch_gemv_any<8>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
     default: e = launch_gemv_any<16>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
+  }
+  if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
+  return FFAI_OK;
+}
+
+int ffai_gemv_f16_qkv_cache(const void* w, const float* bias, int32_t in_dim, const float* x,
+                            int32_t rows, int64_t x_row_stride, float* q, int64_t q_row_stride,
+                            const ffai_kv_cache* c, void* stream) {
+  api_clear_error();
+  if (!w || !x || !q || !c || !c->k || !c->v || !c->lens) return api_fail(FFAI_ERR_INVALID, "null pointer");
+  if (c->dtype != FFAI_F32 && c->dtype != FFAI_F16 && c->dtype != FFAI_BF16)
+    return api_fail(FFAI_ERR_INVALID, "unknown cache dtype");
+  if (c->slots < 1 || c->heads < 1 || c->capacity < 1 || c->head_dim < 8 || c->head_dim % 8)
+    return api_fail(FFAI_ERR_INVALID, "slots, heads, capacity >= 1 and head_dim a multiple of 8");
+  if (c->strides[0] < 0 || c->strides[1] < 0 || c->strides[2] < c->head_dim)
+    return api_fail(FFAI_ERR_INVALID, "bad cache strides");
+  if (in_dim < 8 || in_dim % 8) return api_fail(FFAI_ERR_INVALID, "in_dim must be a multiple of 8");
+  if (rows < 1 || rows > kMaxGemvRows || rows > c->slots)
+    return api_fail(FFAI_ERR_INVALID, "rows must be in [1, 16] and at most the cache's slots");
+  const int64_t n = (int64_t)c->heads * c->head_dim;
+  if (3 * n >= (int64_t(1) << 31) || 3 * n * in_dim >= (int64_t(1) << 40))
+    return api_fail(FFAI_ERR_INVALID, "weights too large");
+  if ((rows > 1 && (x_row_stride < in_dim || q_row_stride < n)) || x_row_stride % 4)
+    return api_fail(FFAI_ERR_INVALID, "bad row strides (x rows need 16-byte alignment)");
+  const size_t es = c->dtype == FFAI_F32 ? 4 : 2;
+  if ((uintptr_t)w % 16 || (uintptr_t)x % 16 || (uintptr_t)q % 4 || (uintptr_t)bias % 4 ||
+      (uintptr_t)c->k % es || (uintptr_t)c->v % es)
+    return api_fail(FFAI_ERR_INVALID, "w and x must be 16-byte aligned, q, bias and the cache "
+                                      "aligned to their elements");
+  const int rc = api_check_device();
+  if (rc != FFAI_OK) return rc;
+  QkvCacheParams p{};
+  p.bias = bias; p.q = q; p.qs = q_row_stride;
+  p.ck = c->k; p.cv = c->v; p.lens = c->lens;
+  p.cs = c->strides[0]; p.ch = c->strides[1]; p.cp = c->strides[2];
+  p.n = (int32_t)n; p.head_dim = c->head_dim; p.capacity = c->capacity;
+  const auto* wp = static_cast<const uint16_t*>(w);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int cdt = c->dtype;  // FFAI_F32 / F16 / BF16 are kF32 / kF16 / kBF16
+  hipError_t e;
+  switch (rows) {
+    case 1: e = launch_qkv_cache<1>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 2: e = launch_qkv_cache<2>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 3: e = launch_qkv_cache<3>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 4: e = launch_qkv_cache<4>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 5: e = launch_qkv_cache<5>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 6: e = launch_qkv_cache<6>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 7: e = launch_qkv_cache<7>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    case 8: e = launch_qkv_cache<8>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
+    default: e = launch_qkv_cache<16>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
   }
   if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
   return FFAI_OK;

@@ -130,6 +130,15 @@ __global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* lens, int slot
   if (s < slots) lens[s] = min(capacity, min(max(lens[s], 0), capacity) + t_new);
 }
 
+// The same for every layer of a layer-stacked cache (blockIdx.y: the layer).
+__global__ __launch_bounds__(256) void kv_advance_layers_kernel(int32_t* lens, int slots,
+                                                                int64_t layer_stride,
+                                                                int capacity, int t_new) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  int32_t* l = lens + (int64_t)blockIdx.y * layer_stride;
+  if (s < slots) l[s] = min(capacity, min(max(l[s], 0), capacity) + t_new);
+}
+
 struct GatherParams {
   char* dk;
   char* dv;
@@ -370,6 +379,27 @@ int ffai_kv_append(const ffai_kv_cache* c, const void* new_k, const void* new_v,
               aligned8(c->v, esize(dt_of(c->dtype)), {0});
   const hipError_t e = dispatch2<AppendLaunch>(sdt, dt_of(c->dtype), p, c->slots,
                                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
+  return FFAI_OK;
+}
+
+int ffai_kv_advance(const ffai_kv_cache* c, int32_t t_new, int32_t layers,
+                    int64_t lens_layer_stride, void* stream) {
+  api_clear_error();
+  int rc = check_cache(c);
+  if (rc != FFAI_OK) return rc;
+  if (t_new < 0) return api_fail(FFAI_ERR_INVALID, "t_new must be >= 0");
+  if (layers < 1 || layers > 65535) return api_fail(FFAI_ERR_INVALID, "layers must be in [1, 65535]");
+  if (layers > 1 && lens_layer_stride < c->slots)
+    return api_fail(FFAI_ERR_INVALID, "lens_layer_stride must separate the layers");
+  if (layers == 1) lens_layer_stride = 0;
+  if (t_new == 0) return FFAI_OK;
+  rc = api_check_device();
+  if (rc != FFAI_OK) return rc;
+  hipLaunchKernelGGL(kv_advance_layers_kernel, dim3((unsigned)((c->slots + 255) / 256), (unsigned)layers),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), c->lens, c->slots,
+                     lens_layer_stride, c->capacity, t_new);
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
   return FFAI_OK;
 }

@@ -36,6 +36,25 @@ class F16Gemv:
 
     __call__ = forward
 
+    def qkv_into_cache(self, x: torch.Tensor, q_out: torch.Tensor, cache,
+                       bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The packed (q; k; v) projection of a decode step (weights (3 * heads * head_dim,
+        in)): q_out (rows, heads * head_dim) f32 gets the q part, and the k and v rows of beam r
+        go into slot r of `cache` (one layer's KVCache) at position lens[r] - 1, the position the
+        step's cache.advance() opened. bias: (3 * heads * head_dim,) f32 or None."""
+        assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
+        n = cache.heads * cache.head_dim
+        assert self.out_dim == 3 * n and cache.layers is None
+        assert q_out.dtype == torch.float32 and q_out.shape == (x.shape[0], n) and q_out.stride(1) == 1
+        if bias is not None:
+            assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == 3 * n
+        c = cache.view()
+        L.check(L.load().ffai_gemv_f16_qkv_cache(
+            self.w.data_ptr(), None if bias is None else bias.data_ptr(), self.in_dim,
+            x.data_ptr(), x.shape[0], x.stride(0), q_out.data_ptr(), q_out.stride(0),
+            ctypes.byref(c), _stream_handle(x)))
+        return q_out
+
 
 class Int8Vocab:
     """Int8Vocab::new quantizes the (vocab, d) embedding matrix on the device once; forward maps

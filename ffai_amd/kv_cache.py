@@ -4,7 +4,8 @@ The reference keeps each decoder layer's self-attention cache as raw (b, L, n_st
 projections grown by Tensor::cat (crates/ffai-mercury/src/asr/text_decoder.rs:652-662),
 re-splits it into heads every step (:840-842), and snapshots/restores it per beam
 (:1350-1381; decoder.rs:559-583). Here a KVCache holds the head-major layout the attention
-kernels read, appended in place (`append`) and reordered by parent beam (`gather_from`);
+kernels read, appended in place (`append`, or `advance` with the rows written by
+gemv.F16Gemv.qkv_into_cache) and reordered by parent beam (`gather_from`);
 `cross_kv_build` prepares the cross-attention cache once per window (:706-707, :770-773).
 """
 
@@ -67,6 +68,14 @@ class KVCache:
         L.check(L.load().ffai_kv_append(ctypes.byref(c), k_new.data_ptr(), v_new.data_ptr(),
                                         _DT[k_new.dtype], k_new.shape[1], k_new.stride(0),
                                         k_new.stride(1), _stream_handle(k_new)))
+
+    def advance(self, t_new: int = 1) -> None:
+        """lens += t_new (saturating at capacity) in every layer: a decode step's length update
+        when F16Gemv.qkv_into_cache writes the step's rows itself."""
+        layers, lls = (1, 0) if self.layers is None else (self.layers, self.lens.stride(0))
+        c = self.view()
+        L.check(L.load().ffai_kv_advance(ctypes.byref(c), t_new, layers, lls,
+                                         _stream_handle(self.lens)))
 
     def gather_from(self, src: "KVCache", parent: torch.Tensor) -> None:
         """Slot i becomes a copy of src's slot parent[i] (a beam step's reorder), in every layer."""

@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "ffai_attn.h"
+#include "ffai_kv.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -33,6 +34,23 @@ extern "C" {
  * agree to f32 rounding, not bit for bit. */
 int ffai_gemv_f16(const void* w, int32_t out_dim, int32_t in_dim, const float* x, int32_t rows,
                   int64_t x_row_stride, float* y, int64_t y_row_stride, void* stream);
+
+/* The self-attention q/k/v projection of a decode step, with the new K/V rows written straight
+ * into the layer's cache: replaces, for single-token steps, the three GEMVs of forward_self
+ * (text_decoder.rs:652-655; QLinear::forward, Half arm, :281-293, with its bias added after the
+ * product) followed by ffai_kv_append of the k and v rows (the Tensor::cat of :657-662).
+ * w: the packed (3 * heads * head_dim, in_dim) f16 weights, rows q, then k, then v; bias: 3 *
+ * heads * head_dim f32 (0 for the bias-free k rows) or NULL. Row r of x (beam r, slot r of the
+ * cache) gives q row r (row stride q_row_stride, f32) and the k and v rows at position
+ * lens[r] - 1 of slot r, converted to the cache dtype by round-to-nearest-even: the step's
+ * ffai_kv_advance runs before the layer, so that position is the one it opened. Per output the
+ * GEMV sum is that of ffai_gemv_f16 and the bias a separate f32 add, so q and the cache rows
+ * equal ffai_gemv_f16 + bias + ffai_kv_append bit for bit, except where the cache was already
+ * full before the advance: the append drops the row, this call replaces the last one. A slot
+ * whose length is 0 gets no row. rows in [1, 16] and at most c->slots; in_dim a multiple of 8. */
+int ffai_gemv_f16_qkv_cache(const void* w, const float* bias, int32_t in_dim, const float* x,
+                            int32_t rows, int64_t x_row_stride, float* q, int64_t q_row_stride,
+                            const ffai_kv_cache* c, void* stream);
 
 /* Int8Vocab::new (vocab_int8.rs:100-170): quantize the (vocab, d) embedding matrix (f32, f16
  * or bf16, row-major) with one scale per `blk` weights: scale = amax / 127 (1 where the block

@@ -14,6 +14,8 @@
  * Here the state lives in HBM in the layout the attention kernels read -- head-major rows
  * (slot, head, position, head_dim) -- and three entry points replace those steps:
  *   ffai_kv_append       <- Tensor::cat + split_heads per step (forward_self, :652-662, :840-842)
+ *   ffai_kv_advance      <- the length half of that step, for every layer at once, when
+ *                           ffai_gemv_f16_qkv_cache (ffai_gemv.h) writes the rows itself
  *   ffai_kv_gather       <- DecoderState save/restore across a beam step (:1350-1381,
  *                           decoder.rs:559-583)
  *   ffai_cross_kv_build  <- the cross-attention cache build (forward_cross, :706-707, :770-773)
@@ -56,6 +58,15 @@ typedef struct ffai_kv_cache {
  * split_heads of the whole cache (:640-643, :840-842). */
 int ffai_kv_append(const ffai_kv_cache* c, const void* new_k, const void* new_v, int32_t src_dtype,
                    int32_t t_new, int64_t src_slot_stride, int64_t src_row_stride, void* stream);
+
+/* Advance the lengths of every layer of a layer-stacked cache by t_new, as ffai_kv_append does
+ * after writing its rows: lens[l * lens_layer_stride + s] = min(capacity, l0 + t_new) with l0
+ * the old length clamped to [0, capacity], for l < layers and s < c->slots (c describes layer
+ * 0). With ffai_gemv_f16_qkv_cache (ffai_gemv.h) a decode step calls it once before its layers,
+ * in place of one append per layer. layers in [1, 65535]; lens_layer_stride >= slots when
+ * layers > 1. */
+int ffai_kv_advance(const ffai_kv_cache* c, int32_t t_new, int32_t layers,
+                    int64_t lens_layer_stride, void* stream);
 
 /* Beam reorder: slot i of dst becomes a copy of slot parent[i] of src (its first
  * src.lens[parent[i]] positions) and dst.lens[i] = src.lens[parent[i]], in each of `layers`

@@ -154,6 +154,8 @@ extern "C" {
     pub fn ffai_kv_gather(dst: *const ffai_kv_cache, src: *const ffai_kv_cache,
                           parent: *const i32, layers: i32, layer_stride: i64,
                           lens_layer_stride: i64, stream: *mut c_void) -> c_int;
+    pub fn ffai_kv_advance(c: *const ffai_kv_cache, t_new: i32, layers: i32,
+                           lens_layer_stride: i64, stream: *mut c_void) -> c_int;
     pub fn ffai_cross_kv_build(k_proj: *const c_void, v_proj: *const c_void, src_dtype: i32,
                                t: i32, heads: i32, head_dim: i32, src_row_stride: i64,
                                k_out: *mut c_void, v_out: *mut c_void, out_dtype: i32,
@@ -171,6 +173,10 @@ extern "C" {
     pub fn ffai_gemv_f16(w: *const c_void, out_dim: i32, in_dim: i32, x: *const f32, rows: i32,
                          x_row_stride: i64, y: *mut f32, y_row_stride: i64,
                          stream: *mut c_void) -> c_int;
+    pub fn ffai_gemv_f16_qkv_cache(w: *const c_void, bias: *const f32, in_dim: i32,
+                                   x: *const f32, rows: i32, x_row_stride: i64, q: *mut f32,
+                                   q_row_stride: i64, c: *const ffai_kv_cache,
+                                   stream: *mut c_void) -> c_int;
     pub fn ffai_vocab_int8_quantize(emb: *const c_void, emb_dtype: i32, vocab: i32, d: i32,
                                     blk: i32, qw: *mut i8, bscale: *mut f32, corr: *mut f32,
                                     stream: *mut c_void) -> c_int;

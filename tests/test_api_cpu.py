@@ -272,6 +272,42 @@ def test_kv_gather_rejects_bad_arguments(lib):
     assert "layer strides" in L.last_error()
 
 
+def test_kv_advance_rejects_bad_arguments(lib):
+    c = _cache()
+
+    def rc(cache=c, t=1, layers=24, lls=5):
+        return lib.ffai_kv_advance(ctypes.byref(cache), t, layers, lls, None)
+
+    assert rc(t=-1) == L.FFAI_ERR_INVALID
+    assert rc(layers=0) == L.FFAI_ERR_INVALID
+    assert rc(layers=65536) == L.FFAI_ERR_INVALID
+    assert rc(lls=4) == L.FFAI_ERR_INVALID             # the layers' lengths would overlap
+    assert "lens_layer_stride" in L.last_error()
+    assert rc(cache=_cache(data=0)) == L.FFAI_ERR_INVALID
+    assert rc(t=0) == L.FFAI_OK                        # nothing to do, nothing launched
+
+
+def test_gemv_qkv_cache_rejects_bad_arguments(lib):
+    c = _cache()   # 5 slots, 16 heads x 64: out_dim 3 x 1024
+
+    def rc(w=FAKE, bias=None, in_dim=1024, x=FAKE, rows=5, xs=1024, q=FAKE, qs=1024, cache=c):
+        return lib.ffai_gemv_f16_qkv_cache(w, bias, in_dim, x, rows, xs, q, qs,
+                                           ctypes.byref(cache), None)
+
+    assert rc(w=None) == L.FFAI_ERR_INVALID
+    assert rc(q=None) == L.FFAI_ERR_INVALID
+    assert rc(in_dim=1020) == L.FFAI_ERR_INVALID       # f16_gemv.rs:101-103's rule
+    assert rc(rows=6) == L.FFAI_ERR_INVALID            # more beams than cache slots
+    assert "slots" in L.last_error()
+    assert rc(rows=17, cache=_cache(slots=20)) == L.FFAI_ERR_INVALID
+    assert rc(qs=1000) == L.FFAI_ERR_INVALID           # q rows shorter than heads * head_dim
+    assert rc(xs=1000) == L.FFAI_ERR_INVALID
+    assert rc(bias=FAKE + 2) == L.FFAI_ERR_INVALID     # misaligned bias
+    assert rc(cache=_cache(dtype=7)) == L.FFAI_ERR_INVALID
+    assert rc(cache=_cache(d=60)) == L.FFAI_ERR_INVALID
+    assert rc(cache=_cache(data=0)) == L.FFAI_ERR_INVALID
+
+
 def test_cross_kv_build_rejects_bad_arguments(lib):
     def rc(t=1500, heads=16, d=64, rs=1024, layout=L.K_TRANSPOSED, odt=L.BF16):
         return lib.ffai_cross_kv_build(FAKE, FAKE, L.F32, t, heads, d, rs, FAKE, FAKE, odt, layout,
