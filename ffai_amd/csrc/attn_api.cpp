@@ -313,12 +313,20 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
     } else if (items > slots && n_tiles >= 8) {
       // Non-causal: a last round of at most a quarter of the slots runs its items in 4 pieces.
       // whisper-small (B8 H12 T1500: 576 items, 512 resident): 75.2 us with the last 64 items
-      // in 4 pieces against 88.0 unsplit (2: 78.1, 6: 87.5); whisper-large-v3 (1920 items, a
-      // last round of 384) stays unsplit (219.9 us; its last 128 items in 2 pieces 212.4,
-      // within the spread of the rounds).
+      // in 4 pieces against 88.0 unsplit (2: 78.1, 6: 87.5).
       const int64_t tail = items % slots;
       if (tail > 0 && 4 * tail <= slots) {
         want = 4; lo = items - tail; hi = items; optional = true;
+      } else if (tail > 0 && 3 * tail >= slots && p.variant == ffai::kWave4x2) {
+        // A last round of at least a third of the slots: the last k items go in n pieces so
+        // that the last round holds exactly one work per slot, tail - k whole items and k * n
+        // pieces. A CU then pairs a whole item with a piece, and the whole item runs alone once
+        // the piece is done. whisper-large-v3 (1920 items, a last round of 384: its last 128 in
+        // 2 pieces, 2048 works): 211.3 us against 215.7 unsplit (5 interleaved rounds; the last
+        // 64 in 3 pieces, also 2048 works, 213.2; 2048 +- 64 or 128 works 215-221).
+        const int64_t n = 2 * tail >= slots ? 2 : 3;
+        const int64_t k = (slots - tail) / (n - 1);
+        if (k >= 1 && k <= tail) { want = n; lo = items - k; hi = items; optional = true; }
       }
     }
   }

@@ -122,9 +122,15 @@ def test_non_finite_or_non_positive_scale_is_an_error(lib, bad):
 
 def test_workspace_only_for_split_shapes(lib):
     n = ctypes.c_size_t(0)
+    # 1024 items of 256 rows: two whole rounds of the 512 resident slots, nothing split
+    whole = desc(lib, L.BF16, L.BF16, L.BF16, 16, 16, 16, 1024, 1024, 64, L.K_TRANSPOSED)
+    assert lib.ffai_attn_workspace_bytes(ctypes.byref(whole), ctypes.byref(n)) == L.FFAI_OK
+    assert n.value == 0
+    # whisper-large-v3: the last 128 of 1920 items in 2 pieces -> the counters plus 128 x 2
+    # partials of 256 rows x (64 + 2) floats
     big = desc(lib, L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED)
     assert lib.ffai_attn_workspace_bytes(ctypes.byref(big), ctypes.byref(n)) == L.FFAI_OK
-    assert n.value == 0
+    assert n.value == 4096 + 128 * 2 * 256 * 66 * 4
     beam = desc(lib, L.BF16, L.BF16, L.F32, 1, 16, 16, 5, 1500, 64, L.K_TRANSPOSED)
     assert lib.ffai_attn_workspace_bytes(ctypes.byref(beam), ctypes.byref(n)) == L.FFAI_OK
     # decode shape: per-split partials (O and (m, l) for 5 rows x 16 heads) plus counters
@@ -386,9 +392,10 @@ def _plan(lib, *args, causal=0):
 
 
 @pytest.mark.parametrize("args,causal,info,splits", [
-    # whisper-large-v3 encoder: 1920 items of 256 rows, none split (a last round of 384 of 512)
+    # whisper-large-v3 encoder: 1920 items of 256 rows, a last round of 384 of 512 slots: the
+    # last 128 items in 2 pieces, so that the last round holds 256 whole items + 256 pieces
     ((L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED), 0,
-     [0, 2, 1, 24, 1920], [1920, 0, 0]),
+     [0, 2, 2, 12, 2048], [1920, 1792, 1920]),
     # whisper-small: 576 items on 512 resident, the last 64 in 4 pieces
     ((L.BF16, L.BF16, L.BF16, 8, 12, 12, 1500, 1500, 64, L.K_TRANSPOSED), 0,
      [0, 2, 4, 6, 768], [576, 512, 576]),
@@ -430,8 +437,8 @@ def test_split_override_and_its_workspace(lib):
         assert n.value == 4096 + 100 * 3 * 256 * 66 * 4   # counters + partials of 300 pieces
         L.set_fwd_split_override(-1, 1)                     # nothing split
         assert _plan(lib, *args)[1] == [1920, 0, 0]
-        L.set_fwd_split_override(0, 0)
-        assert _plan(lib, *args)[1] == [1920, 0, 0]
+        L.set_fwd_split_override(0, 0)                      # the planner's own layout
+        assert _plan(lib, *args)[1] == [1920, 1792, 1920]
         assert L.get_fwd_split_override() == (0, 0)
     finally:
         L.set_fwd_split_override(*prev)

@@ -135,8 +135,12 @@ def test_sixteen_windows_in_one_pass_stay_in_bounds(packed):
     assert 2 * ((k_rows - 1) * k_st + 8 * 7 + 7) < 2 ** 32
     items = b * h * -(-s // 256)
     assert items < 2 ** 31 and items * -(-s // BN) < 2 ** 30
-    # no key-split partials at this size (1920 items, a last round of 384 of 512 resident)
-    assert attn_ws_bytes(lib, b, s, n, h, packed) == 0
+    # the attention's own workspace at this size (1920 items, a last round of 384 of 512
+    # resident: the last 128 items in 2 pieces) is the split counters plus 256 partials, which
+    # fit the region reserved for it and the kernel's 32-bit buffer offsets
+    ws = attn_ws_bytes(lib, b, s, n, h, packed)
+    assert ws == COUNTER_BYTES + 128 * 2 * 256 * (hd + 2) * 4
+    assert ws <= z["attn"][1] - z["attn"][0] and ws < 2 ** 31
 
 
 def test_one_pass_above_1500_rows_is_refused():

@@ -97,7 +97,8 @@ def test_whisper_small_full_size(gpu, dtype):
 def test_whisper_large_v3_full_size(gpu):
     q, kt, v = _encoder_case(4, 16, 20, 1500, 64, torch.bfloat16)
     _run_encoder(gpu, q, kt, v, torch.bfloat16, torch.bfloat16,
-                 {"kernel": "fwd", "shape": "wave4x2", "splits": 1, "workgroups": 1920})
+                 {"kernel": "fwd", "shape": "wave4x2", "splits": 2, "workgroups": 2048,
+                  "split_items": (1792, 1920)})
 
 
 def _rotate_pairs(x: np.ndarray, rng) -> np.ndarray:
