@@ -249,6 +249,13 @@ def pipes_bench(torch, iters=4096, waves_per_simd=(1, 2, 4)):
 # Beam-5 decode step (whisper-medium: 24 layers, 16 heads, D=64)
 # ------------------------------------------------------------------------------------------
 
+# The decode step keeps the cross-attention cache's K as rows (heads, frames, head_dim): that
+# cache is built once per window by ffai_cross_kv_build, which writes either layout, and rows are
+# whole 128-byte lines per key where K^T rows (3000 bytes apart at 1500 frames) straddle lines
+# (beam-5 cross-attention launch, graphs: 7.9 against 9.1 us).
+CROSS_K_TRANSPOSED = False
+
+
 def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=448, layers=24,
                  sets=3, graphs=True):
     dev = torch.device("cuda:0")
@@ -266,7 +273,8 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
             v_self = torch.randn(beams, H, cap, D, generator=gd, device=dev).to(bf)
             lens = lens_cpu[l].to(dev)
             q_x = torch.randn(beams, H, 1, D, generator=gd, device=dev).to(bf)
-            kt_x = torch.randn(1, H, D, T_enc, generator=gd, device=dev).to(bf)
+            kt_x = torch.randn(*((1, H, D, T_enc) if CROSS_K_TRANSPOSED else (1, H, T_enc, D)),
+                               generator=gd, device=dev).to(bf)
             v_x = torch.randn(1, H, T_enc, D, generator=gd, device=dev).to(bf)
             o_self = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
             o_x = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
@@ -277,15 +285,16 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
     ws_self = torch.zeros(max(1, fa.workspace_bytes(qs, ks, vs, os_, scale=scale, kv_lens=ls)),
                           dtype=torch.uint8, device=dev)
     ws_x = torch.zeros(max(1, fa.workspace_bytes(qx.permute(2, 1, 0, 3), ktx, vx,
-                                                 ox.permute(2, 1, 0, 3), k_transposed=True,
+                                                 ox.permute(2, 1, 0, 3),
+                                                 k_transposed=CROSS_K_TRANSPOSED,
                                                  scale=scale)), dtype=torch.uint8, device=dev)
 
     def step(layer_bufs):
         for (q_self, k_self, v_self, lens, o_self, q_x, kt_x, v_x, o_x) in layer_bufs:
             fa.attention(q_self, k_self, v_self, scale=scale, kv_lens=lens, out=o_self,
                          workspace=ws_self)
-            fa.attention(q_x.permute(2, 1, 0, 3), kt_x, v_x, k_transposed=True, scale=scale,
-                         out=o_x.permute(2, 1, 0, 3), workspace=ws_x)
+            fa.attention(q_x.permute(2, 1, 0, 3), kt_x, v_x, k_transposed=CROSS_K_TRANSPOSED,
+                         scale=scale, out=o_x.permute(2, 1, 0, 3), workspace=ws_x)
 
     # capture one HIP graph per buffer set: the step's 48 attention calls replay without
     # host-side dispatch (the kernels use no memset; the workspaces are preallocated). Without
@@ -327,7 +336,8 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
         "self_bytes_per_step": self_bytes,
         "gbps": step_bytes / (us_step * 1e-6) / 1e9,
         "hbm_frac": step_bytes / (us_step * 1e-6) / 1e9 / PEAK_HBM_GBPS,
-        "launches_per_step": 2 * layers * 2,
+        "launches_per_step": 2 * layers,
+        "cross_k_layout": "transposed" if CROSS_K_TRANSPOSED else "rows",
         "mean_self_len": float(lens_cpu.float().mean()),
         "buffer_sets": sets,
         "hip_graphs": graphs,
@@ -346,7 +356,7 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
     (self-attention over the beams' caches, cross-attention over the window's shared cache).
     All beams of a step share one length, as in beam search; lengths start so that the timed
     steps are centred on `mid_len`. Also times the per-window cross-attention cache build of
-    the 24 layers (f32 projections -> bf16 K^T and V)."""
+    the 24 layers (f32 projections -> bf16 K and V, K as rows)."""
     from ffai_amd.kv_cache import KVCache, cross_kv_build
 
     dev = torch.device("cuda:0")
@@ -368,7 +378,7 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
                       torch.randn(beams, H, 1, D, generator=gd, device=dev).to(bf)))
         kp = torch.randn(T_enc, H * D, generator=gd, device=dev)
         vp = torch.randn(T_enc, H * D, generator=gd, device=dev)
-        xs.append((kp, vp) + cross_kv_build(kp, vp, H, bf, k_transposed=True))
+        xs.append((kp, vp) + cross_kv_build(kp, vp, H, bf, k_transposed=CROSS_K_TRANSPOSED))
     parent = torch.randint(0, beams, (beams,), generator=g, dtype=torch.int32).to(dev)
     o_self = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
     o_x = torch.empty(beams, H, 1, D, device=dev, dtype=torch.float32)
@@ -377,7 +387,7 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
                                                     kv_lens=k0.lens)), dtype=torch.uint8, device=dev)
     ws_x = torch.zeros(max(1, fa.workspace_bytes(projs[0][3].permute(2, 1, 0, 3), xs[0][2][None],
                                                  xs[0][3][None], o_x.permute(2, 1, 0, 3),
-                                                 k_transposed=True, scale=scale)),
+                                                 k_transposed=CROSS_K_TRANSPOSED, scale=scale)),
                        dtype=torch.uint8, device=dev)
 
     def step(phase, attend):
@@ -390,8 +400,8 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
                 fa.attention(qs, c.k, c.v, scale=scale, kv_lens=c.lens, out=o_self,
                              workspace=ws_self)
                 fa.attention(qx.permute(2, 1, 0, 3), xs[l][2][None], xs[l][3][None],
-                             k_transposed=True, scale=scale, out=o_x.permute(2, 1, 0, 3),
-                             workspace=ws_x)
+                             k_transposed=CROSS_K_TRANSPOSED, scale=scale,
+                             out=o_x.permute(2, 1, 0, 3), workspace=ws_x)
         nxt.gather_from(cur, parent)   # every layer's reorder in one launch
 
     def timed(attend):
@@ -478,7 +488,7 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
 
     def build_all():
         for kp, vp, kx, vx in xs:
-            cross_kv_build(kp, vp, H, bf, k_transposed=True, out=(kx, vx))
+            cross_kv_build(kp, vp, H, bf, k_transposed=CROSS_K_TRANSPOSED, out=(kx, vx))
 
     build_all()
     torch.cuda.synchronize()
@@ -501,14 +511,14 @@ def decode_state_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500
     pq = torch.randn(1, H, P, D, generator=gd, device=dev).to(bf)
     po = torch.empty(1, H, P, D, device=dev, dtype=torch.float32)
     pws = torch.zeros(max(1, fa.workspace_bytes(pq, xs[0][2][None], xs[0][3][None], po,
-                                                k_transposed=True, scale=scale)),
+                                                k_transposed=CROSS_K_TRANSPOSED, scale=scale)),
                       dtype=torch.uint8, device=dev)
 
     def prompt_step():
         for l in range(layers):
             self_attention_step(pstack.layer(l), pq, pk, pv, 0, scale, out=po, workspace=pws)
-            fa.attention(pq, xs[l][2][None], xs[l][3][None], k_transposed=True, scale=scale,
-                         out=po, workspace=pws)
+            fa.attention(pq, xs[l][2][None], xs[l][3][None], k_transposed=CROSS_K_TRANSPOSED,
+                         scale=scale, out=po, workspace=pws)
 
     pstack.lens.zero_()
     torch.cuda.synchronize()

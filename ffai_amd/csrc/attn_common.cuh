@@ -162,6 +162,14 @@ __device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x007
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
+// Workgroup and work-item indices read straight from the registers the hardware loads at
+// launch. (blockIdx / threadIdx go through device-library functions that this toolchain leaves
+// out of line: every kernel would start with calls into code far from its own, each a cold
+// instruction fetch before the first load is issued.) Work-items: one-dimensional workgroups.
+__device__ __forceinline__ int wg_id_x() { return (int)__builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int wg_id_y() { return (int)__builtin_amdgcn_workgroup_id_y(); }
+__device__ __forceinline__ int wg_id_z() { return (int)__builtin_amdgcn_workgroup_id_z(); }
+__device__ __forceinline__ int item_id() { return (int)__builtin_amdgcn_workitem_id_x(); }
 
 template <int DT>
 __device__ __forceinline__ f32x16 mfma16(u32x4 a, u32x4 b, f32x16 c) {

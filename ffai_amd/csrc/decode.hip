@@ -8,9 +8,8 @@ namespace {
 
 template <int MODE, int OUTT, int D, bool KT, int NWD>
 hipError_t launch_dec(const DecodeParams& p, hipStream_t s) {
-  const unsigned grid = (unsigned)((p.n_work + 7) / 8 * 8);  // whole XCD rounds
-  hipLaunchKernelGGL((decode_kernel<MODE, OUTT, D, KT, NWD>), dim3(grid), dim3(NWD * 64), 0, s,
-                     p);
+  const dim3 grid((unsigned)p.n_split, (unsigned)p.Hkv, (unsigned)p.B);  // (split, kv-head, batch)
+  hipLaunchKernelGGL((decode_kernel<MODE, OUTT, D, KT, NWD>), grid, dim3(NWD * 64), 0, s, p);
   return hipGetLastError();
 }
 

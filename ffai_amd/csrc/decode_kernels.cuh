@@ -55,18 +55,21 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   static_assert((WBUF * 2) % 16 == 0 && (KBUF * 2) % 16 == 0, "16-byte aligned regions");
   __shared__ __attribute__((aligned(16))) uint16_t lds[NWD * WBUF];
 
-  // ---- which (batch, kv-head, key split): splits of one unit run on one XCD
-  const int hw = blockIdx.x;
-  const int work = (hw & 7) * (int)(gridDim.x >> 3) + (hw >> 3);
-  if (work >= p.n_work) return;
-  const int split = work % p.n_split;
-  const int unit = work / p.n_split;
-  const int hk = unit % p.Hkv;
-  const int b = unit / p.Hkv;
+  // ---- which (batch, kv-head, key split): the grid is (splits, kv-heads, batch), so the
+  //      indices are the workgroup's own and its operand addresses are scalar arithmetic (a
+  //      division of a flat index cost ~0.3 us of dependent vector instructions before the first
+  //      K/V load could be issued)
+  const int split = wg_id_x();
+  const int hk = wg_id_y();
+  const int b = wg_id_z();
+  const int unit = b * p.Hkv + hk;
 
-  const int tid = threadIdx.x;
+  const int tid = item_id();
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave-uniform, and made visibly so: the tile choices below are then scalar branches, and the
+  // compiler does not wait on one branch's loads before another's (it did: the register-staging
+  // loads of the tail path made it await the Q loads before issuing any K/V DMA)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;
   const int n32 = lane & 31;  // this lane's query row of the unit (MFMA column)
   const int R = p.group * p.Tq;
@@ -76,29 +79,18 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
 
   int kv_end = p.Tk;
   if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
+  kv_end = __builtin_amdgcn_readfirstlane(kv_end);  // uniform (one batch item per workgroup)
   int kv_blk = kv_end;  // keys any row of the unit may see
   if (p.causal) kv_blk = min(kv_end, max(0, p.q_offset + p.Tq));
   const int n_tiles = (kv_blk + BN - 1) / BN;
   const int t_begin = split * p.tiles_per_split;
   const int t_end = min(n_tiles, t_begin + p.tiles_per_split);
-  const int iters = t_end > t_begin ? (t_end - t_begin + NWD - 1) / NWD : 0;  // uniform
+  const int iters = t_end > t_begin ? (t_end - t_begin + NWD - 1) / NWD : 0;
   const float sl2 = p.scale_log2;
   const int lim = p.causal ? min(kv_end - 1, p.q_offset + t_row) : kv_end - 1;
 
   const uint16_t* kp = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + hk * p.k_sh;
   const uint16_t* vp = reinterpret_cast<const uint16_t*>(p.v) + b * p.v_sb + hk * p.v_sh;
-
-  // ---- Q fragments: B operand of S^T, step s: d = 16s + 8g .. +7 of row rn
-  u32x4 qf[D / 16];
-  {
-    const uint16_t* qr = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_sb + h_row * p.q_sh +
-                         (int64_t)t_row * p.q_st;
-#pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const u32x4 x = ld16(qr + 16 * s + 8 * g);
-      qf[s] = n32 < R ? x : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
 
   f32x16 oacc[D / 32];
 #pragma unroll
@@ -184,18 +176,32 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       lds_dma16_sbase<true>(vbase, off, vla + j * 1024);
     }
   };
-  // After a clamped K^T DMA has landed: the valid keys of the 8-key chunk that crosses the
-  // operand's end, element by element.
-  auto patch_kt_end = [&](int it) {
+  // The valid keys of the 8-key K^T chunk that crosses the operand's end, element by element:
+  // loaded together with the clamped DMA (so both share one memory round trip) and written
+  // over the DMA's stand-in once it has landed. Each lane holds its d-rows' (at most 7) keys.
+  constexpr int PROWS = D / 64;
+  uint16_t patch[PROWS][7];
+  auto patch_kt_load = [&]() {
+    const int klast = kv_end - 1;
+    const int s0 = klast & ~7;
+#pragma unroll
+    for (int i = 0; i < PROWS; ++i) {
+      const uint16_t* row = kp + (int64_t)(lane + 64 * i) * p.k_st;
+#pragma unroll
+      for (int x = 0; x < 7; ++x) patch[i][x] = row[min(s0 + x, klast)];
+    }
+  };
+  auto patch_kt_store = [&](int it) {
     const int kb = it * BN;
     const int klast = kv_end - 1;
     const int s0 = klast & ~7;
-    if (s0 + 8 <= p.Tk) return;  // that chunk was read whole
-    for (int d = lane; d < D; d += 64) {
-      const uint16_t* row = kp + (int64_t)d * p.k_st;
-      for (int k = s0; k <= klast; ++k) {
-        const int col = k - kb;
-        kl[d * KTROW + 8 * swz_kt(d, col >> 3) + (col & 7)] = row[k];
+#pragma unroll
+    for (int i = 0; i < PROWS; ++i) {
+      const int d = lane + 64 * i;
+#pragma unroll
+      for (int x = 0; x < 7; ++x) {
+        const int col = s0 + x - kb;
+        if (s0 + x <= klast) kl[d * KTROW + 8 * swz_kt(d, col >> 3) + (col & 7)] = patch[i][x];
       }
     }
   };
@@ -258,27 +264,56 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     }
   };
 
+  // A ragged tail that still lies inside the operand's rows (a per-beam cache shorter than its
+  // capacity) comes by DMA too. Its keys past the end are masked below, but their V rows may hold
+  // anything (inf, NaN) and a masked weight of 0 times NaN is NaN: they are cleared in LDS once
+  // the DMA has landed. (K^T only) the chunk that crosses the operand's end is not read whole by
+  // the DMA and is patched.
+  auto tail_dma_of = [&](int kb) { return kb + BN > kv_end && kb + BN <= p.Tk; };
+  auto end_dma_of = [&](int kb) { return kb + BN > p.Tk && kb + 8 <= p.Tk; };
+  auto patch_end_of = [&](int kb) {
+    return KT && end_dma_of(kb) && ((kv_end - 1) & ~7) + 8 > p.Tk;
+  };
+  // Issue tile `it`'s loads (by DMA, or through registers for a short end).
+  auto issue_tile = [&](int it) {
+    const int kb = it * BN;
+    if (kb + BN <= kv_end || tail_dma_of(kb)) dma_tile(it);
+    else if (end_dma_of(kb)) dma_tile_clamped(it);
+    else stage_tile(it);
+    if (patch_end_of(kb)) patch_kt_load();
+  };
+  // The wave's first tile goes out before the Q loads: the DMA is a compiler barrier for memory
+  // accesses, so nothing is outstanding when it is issued. (Issued after them, the compiler made
+  // the DMA wait for the Q loads: registers it reuses were load targets on the register-staging
+  // path, and one in-order counter covers both.)
+  if (iters > 0 && t_begin + wave < t_end) issue_tile(t_begin + wave);
+  // ---- Q fragments: B operand of S^T, step s: d = 16s + 8g .. +7 of row rn. Issued after the
+  //      wave's first K/V loads (below). Columns past the unit's R rows repeat row R - 1: each
+  //      column's scores, weights and sums stay in that column, and only the first R are ever
+  //      read back.
+  u32x4 qf[D / 16];
+  {
+    const uint16_t* qr = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_sb + h_row * p.q_sh +
+                         (int64_t)t_row * p.q_st;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) qf[s] = ld16(qr + 16 * s + 8 * g);
+  }
+
 #pragma unroll 1
   for (int i = 0; i < iters; ++i) {
     const int it = t_begin + wave + NWD * i;
     const bool has = it < t_end;  // wave-uniform
     const int kb = it * BN;
     if (!has) continue;
-    // the tile region is this wave's own: reuse needs only its own earlier LDS reads done
-    if (i > 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    // A ragged tail that still lies inside the operand's rows (a per-beam cache shorter than
-    // its capacity) comes by DMA too. Its keys past the end are masked below, but their V rows
-    // may hold anything (inf, NaN) and a masked weight of 0 times NaN is NaN: they are cleared
-    // in LDS once the DMA has landed.
-    const bool tail_dma = kb + BN > kv_end && kb + BN <= p.Tk;
-    const bool end_dma = kb + BN > p.Tk && kb + 8 <= p.Tk;
-    if (kb + BN <= kv_end || tail_dma) dma_tile(it);
-    else if (end_dma) dma_tile_clamped(it);
-    else stage_tile(it);
-    vm_wait_all();
-    if constexpr (KT) {
-      if (end_dma) patch_kt_end(it);
+    if (i > 0) {
+      // the tile region is this wave's own: reuse needs only its own earlier LDS reads done
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      issue_tile(it);
     }
+    const bool tail_dma = tail_dma_of(kb), end_dma = end_dma_of(kb);
+    const bool patch_end = patch_end_of(kb);
+    vm_wait_all();
+    if (patch_end) patch_kt_store(it);
     if (tail_dma || end_dma) {
       constexpr int RU = D / 8;  // 16-byte units per V row; the swizzle stays within a row
       for (int u = max(0, kv_end - kb) * RU + lane; u < BN * RU; u += 64)
@@ -328,8 +363,10 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     const float corr = (m_new == kNegInf) ? 1.f : fast_exp2(m_s - m_new);
     m_s = m_new;
     const float mc = (m_new == kNegInf) ? 0.f : m_new;
+    if (i > 0) {  // the first tile finds the accumulator still zero (wave-uniform)
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= corr;
+      for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= corr;
+    }
     u32x4 pf[4];
     float rs = 0.f;
 #pragma unroll
@@ -372,16 +409,19 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   float* mbase = reinterpret_cast<float*>(lds);
   {
     float* mb = mbase + wave * (WBUF / 2);
+    const float l_tot = partner_sum(l_run);  // the whole wave takes part (a lane swap)
+    // only the unit's R rows are read back: the other columns' lanes write nothing
+    if (n32 < R) {
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<f32x4*>(&mb[n32 * OROW + 32 * dt + 8 * r + 4 * g]) =
-            f32x4{oacc[dt][4 * r], oacc[dt][4 * r + 1], oacc[dt][4 * r + 2], oacc[dt][4 * r + 3]};
-    const float l_tot = partner_sum(l_run);
-    if (g == 0) {
-      mb[32 * OROW + n32] = m_s;
-      mb[32 * OROW + 32 + n32] = l_tot;
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<f32x4*>(&mb[n32 * OROW + 32 * dt + 8 * r + 4 * g]) =
+              f32x4{oacc[dt][4 * r], oacc[dt][4 * r + 1], oacc[dt][4 * r + 2], oacc[dt][4 * r + 3]};
+      if (g == 0) {
+        mb[32 * OROW + n32] = m_s;
+        mb[32 * OROW + 32 + n32] = l_tot;
+      }
     }
   }
   __syncthreads();
@@ -457,7 +497,8 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   const int64_t uml = o_floats + (int64_t)unit * S * R * 2;   // and its first (m, l) pair
   // Online log-sum-exp merge over the splits, eight at a time: the eight splits' device-scope
   // loads are issued together (clamped to the last split; those past it count as empty), then
-  // merged in split order, so one round trip covers eight partials.
+  // merged in split order, so one round trip covers eight partials. (Sixteen at a time measured
+  // slower at 8 and 12 splits: the unrolled merge doubles the code a cold workgroup fetches.)
   constexpr int KS = 8;
 #pragma unroll 1
   for (int it = tid; it < items; it += NWD * 64) {

@@ -90,8 +90,8 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restric
                                                        const float* __restrict__ x, int rows,
                                                        int64_t xs, float* __restrict__ y,
                                                        int64_t ys) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int o = blockIdx.x * 4 + wave;
+  const int tid = item_id(), lane = tid & 63, wave = tid >> 6;
+  const int o = wg_id_x() * 4 + wave;
   if (o >= out_dim) return;
   float acc[R];
   gemv_row<R>(w + (int64_t)o * in_dim, in_dim, x, rows, xs, lane, acc);
@@ -124,8 +124,8 @@ __global__ __launch_bounds__(256) void gemv_f16_qkv_kernel(const uint16_t* __res
                                                            int in_dim,
                                                            const float* __restrict__ x, int rows,
                                                            int64_t xs, QkvCacheParams p) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int o = blockIdx.x * 4 + wave;
+  const int tid = item_id(), lane = tid & 63, wave = tid >> 6;
+  const int o = wg_id_x() * 4 + wave;
   if (o >= 3 * p.n) return;
   float acc[R];
   gemv_row<R>(w + (int64_t)o * in_dim, in_dim, x, rows, xs, lane, acc);
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void vocab_quantize_kernel(const store_t<DT>* 
   // as operators in this scope (the contract setting follows the source location of each
   // operation; header helpers such as __fmul_rn keep the default).
 #pragma clang fp contract(off)
-  const int v = blockIdx.x * 256 + threadIdx.x;
+  const int v = wg_id_x() * 256 + item_id();
   if (v >= vocab) return;
   const int nb = d / blk;
   const store_t<DT>* row = emb + (int64_t)v * d;
@@ -231,24 +231,24 @@ __global__ __launch_bounds__(256) void vocab_act_quant_kernel(const float* __res
                                                               int8_t* __restrict__ xu,
                                                               float* __restrict__ sx_out) {
 #pragma clang fp contract(off)
-  const int r = blockIdx.x;
+  const int r = wg_id_x();
   const float* xr = x + r * xs;
   __shared__ float red[256];
   float m = 0.f;
-  for (int k = threadIdx.x; k < d; k += 256) m = fmaxf(m, fabsf(xr[k]));
-  red[threadIdx.x] = m;
+  for (int k = item_id(); k < d; k += 256) m = fmaxf(m, fabsf(xr[k]));
+  red[item_id()] = m;
   __syncthreads();
   for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+    if (item_id() < s) red[item_id()] = fmaxf(red[item_id()], red[item_id() + s]);
     __syncthreads();
   }
   const float amax = red[0];
   const float sx = amax > 0.f ? __fdiv_rn(amax, 63.f) : 1.f;
-  for (int k = threadIdx.x; k < d; k += 256) {
+  for (int k = item_id(); k < d; k += 256) {
     const float qf = fminf(fmaxf(round_away(__fdiv_rn(xr[k], sx)), -64.f), 63.f);
     xu[(int64_t)r * d_pad + k] = (int8_t)((int)qf + 64);
   }
-  if (threadIdx.x == 0) sx_out[r] = sx;
+  if (item_id() == 0) sx_out[r] = sx;
 }
 
 // Workgroup: kVocabRowsPerWg vocabulary rows (4 per wave). Phase 1: lane l takes 16-byte chunks
@@ -264,11 +264,11 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
 #pragma clang fp contract(off)  // separately rounded multiply and add, as in the reference
   extern __shared__ int bs_lds[];  // [rows][kVocabRowsPerWg][nb]
   const int nb = d / blk;
-  const int v0 = blockIdx.x * kVocabRowsPerWg;
+  const int v0 = wg_id_x() * kVocabRowsPerWg;
   const int n_bs = rows * kVocabRowsPerWg * nb;
-  for (int i = threadIdx.x; i < n_bs; i += 256) bs_lds[i] = 0;
+  for (int i = item_id(); i < n_bs; i += 256) bs_lds[i] = 0;
   __syncthreads();
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = item_id() >> 6, lane = item_id() & 63;
   const int chunks = d / 16;
   for (int j = 0; j < kVocabRowsPerWg / 4; ++j) {
     const int rl = wave * (kVocabRowsPerWg / 4) + j;  // row within the workgroup
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
     }
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < rows * kVocabRowsPerWg; t += 256) {
+  for (int t = item_id(); t < rows * kVocabRowsPerWg; t += 256) {
     const int r = t / kVocabRowsPerWg, rl = t % kVocabRowsPerWg;
     const int v = v0 + rl;
     if (v >= vocab) continue;

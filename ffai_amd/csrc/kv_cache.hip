@@ -92,19 +92,19 @@ struct AppendParams {
 // workgroups of one slot cannot order their reads of lens before its update).
 template <int SRC, int DST>
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
-  const int s = blockIdx.x;
+  const int s = wg_id_x();
   // a length outside [0, capacity] (corrupt or uninitialised) is clamped, as the gather does, so
   // no row lands before the slot's cache or past it
   const int len0 = min(max(p.lens[s], 0), p.capacity);
   const int row_units = p.heads * p.head_dim / 8;
   const int units = p.t_new * row_units;
-  const int u_begin = blockIdx.y * p.units_per_block;
+  const int u_begin = wg_id_y() * p.units_per_block;
   const int u_end = min(units, u_begin + p.units_per_block);
   const auto* sk = reinterpret_cast<const store_t<SRC>*>(p.src_k) + (int64_t)s * p.src_ss;
   const auto* sv = reinterpret_cast<const store_t<SRC>*>(p.src_v) + (int64_t)s * p.src_ss;
   auto* dk = reinterpret_cast<store_t<DST>*>(p.k) + (int64_t)s * p.ks;
   auto* dv = reinterpret_cast<store_t<DST>*>(p.v) + (int64_t)s * p.ks;
-  for (int u = u_begin + threadIdx.x; u < u_end; u += 256) {
+  for (int u = u_begin + item_id(); u < u_end; u += 256) {
     const int t = u / row_units;
     const int col = (u - t * row_units) * 8;  // h * head_dim + d
     const int h = col / p.head_dim, d = col - h * p.head_dim;
@@ -120,13 +120,13 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   }
   if (p.advance) {
     __syncthreads();
-    if (threadIdx.x == 0) p.lens[s] = min(p.capacity, len0 + p.t_new);
+    if (item_id() == 0) p.lens[s] = min(p.capacity, len0 + p.t_new);
   }
 }
 
 __global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* lens, int slots, int capacity,
                                                          int t_new) {
-  const int s = blockIdx.x * 256 + threadIdx.x;
+  const int s = wg_id_x() * 256 + item_id();
   if (s < slots) lens[s] = min(capacity, min(max(lens[s], 0), capacity) + t_new);
 }
 
@@ -134,8 +134,8 @@ __global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* lens, int slot
 __global__ __launch_bounds__(256) void kv_advance_layers_kernel(int32_t* lens, int slots,
                                                                 int64_t layer_stride,
                                                                 int capacity, int t_new) {
-  const int s = blockIdx.x * 256 + threadIdx.x;
-  int32_t* l = lens + (int64_t)blockIdx.y * layer_stride;
+  const int s = wg_id_x() * 256 + item_id();
+  int32_t* l = lens + (int64_t)wg_id_y() * layer_stride;
   if (s < slots) l[s] = min(capacity, min(max(l[s], 0), capacity) + t_new);
 }
 
@@ -164,15 +164,15 @@ template <int ES>
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
   using elem_t = std::conditional_t<ES == 4, uint32_t, uint16_t>;
   constexpr int kPer = 4;  // units per thread per pass, for K and for V
-  const int blk = blockIdx.x % p.n_blk;
-  const int h = (blockIdx.x / p.n_blk) % p.heads;
-  const int i = blockIdx.x / (p.n_blk * p.heads);
-  const int64_t lo = (int64_t)blockIdx.y * p.layer_stride;
-  const int32_t* slens = p.slens + (int64_t)blockIdx.y * p.lens_layer_stride;
+  const int blk = wg_id_x() % p.n_blk;
+  const int h = (wg_id_x() / p.n_blk) % p.heads;
+  const int i = wg_id_x() / (p.n_blk * p.heads);
+  const int64_t lo = (int64_t)wg_id_y() * p.layer_stride;
+  const int32_t* slens = p.slens + (int64_t)wg_id_y() * p.lens_layer_stride;
   const int par = min(max(p.parent[i], 0), p.src_slots - 1);
   const int len = min(max(slens[par], 0), p.capacity);
-  if (blk == 0 && h == 0 && threadIdx.x == 0)
-    p.dlens[(int64_t)blockIdx.y * p.lens_layer_stride + i] = len;
+  if (blk == 0 && h == 0 && item_id() == 0)
+    p.dlens[(int64_t)wg_id_y() * p.lens_layer_stride + i] = len;
   const int pos0 = blk * 64;
   if (pos0 >= len) return;
   const int n = min(64, len - pos0) * p.row_units;
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherParams p) {
   char* dk = p.dk + lo + (int64_t)i * p.ds + (int64_t)h * p.dh + (int64_t)pos0 * p.dp;
   char* dv = p.dv + lo + (int64_t)i * p.ds + (int64_t)h * p.dh + (int64_t)pos0 * p.dp;
   const int ub = p.vec ? 16 : ES;  // bytes per unit
-  for (int base = threadIdx.x; base < n; base += 256 * kPer) {
+  for (int base = item_id(); base < n; base += 256 * kPer) {
     if (p.vec) {
       u32x4 a[kPer], b[kPer];
 #pragma unroll
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void cross_rows_kernel(const void* src, void* 
   const int64_t units = (int64_t)p.t * row_units;
   const auto* s = reinterpret_cast<const store_t<SRC>*>(src);
   auto* o = reinterpret_cast<store_t<DST>*>(dst);
-  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+  for (int64_t u = (int64_t)wg_id_x() * 256 + item_id(); u < units; u += (int64_t)gridDim.x * 256) {
     const int t = (int)(u / row_units);
     const int col = (int)(u - (int64_t)t * row_units) * 8;
     const int h = col / p.head_dim, d = col - h * p.head_dim;
@@ -248,12 +248,12 @@ __global__ __launch_bounds__(256) void cross_rows_kernel(const void* src, void* 
 template <int SRC, int DST>
 __global__ __launch_bounds__(256) void cross_kt_kernel(CrossParams p) {
   __shared__ float tile[64][128 + 1];
-  const int tb = blockIdx.x % p.n_tblk, h = blockIdx.x / p.n_tblk;
+  const int tb = wg_id_x() % p.n_tblk, h = wg_id_x() / p.n_tblk;
   const int t0 = tb * 64;
   const int rows = min(64, p.t - t0);
   const int du = p.head_dim / 8;
   const auto* s = reinterpret_cast<const store_t<SRC>*>(p.sk);
-  for (int u = threadIdx.x; u < rows * du; u += 256) {
+  for (int u = item_id(); u < rows * du; u += 256) {
     const int r = u / du, d = (u - r * du) * 8;
     float x[8];
     load8<SRC>(s + (int64_t)(t0 + r) * p.src_rs + h * p.head_dim + d, p.src_vec, x);
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(256) void cross_kt_kernel(CrossParams p) {
   __syncthreads();
   auto* o = reinterpret_cast<store_t<DST>*>(p.k) + (int64_t)h * p.head_dim * p.t;
   // one output element per thread and step: row d, frame t0 + c
-  for (int u = threadIdx.x; u < p.head_dim * 64; u += 256) {
+  for (int u = item_id(); u < p.head_dim * 64; u += 256) {
     const int d = u / 64, c = u % 64;
     if (c >= rows) continue;
     const float x = tile[c][d];

@@ -154,7 +154,7 @@ def test_qwen2_vl_causal_prefill_full_size(gpu):
 def test_beam5_decode_step_shapes(gpu):
     """One layer of the bench's beam-5 step: self-attention (5 beams x 16 heads over ragged bf16
     caches of capacity 448, lengths U{1..448}) and cross-attention (the 5 beams as the query rows
-    of one 16-head unit each over 1500 shared frames, K^T), f32 outputs."""
+    of one 16-head unit each over 1500 shared frames, K transposed and as rows), f32 outputs."""
     rng = np.random.default_rng(3)
     beams, h, d, cap, frames = 5, 16, 64, 448, 1500
     scale = d ** -0.5
@@ -179,13 +179,16 @@ def test_beam5_decode_step_shapes(gpu):
     qx = round_bf16(rng.standard_normal((1, h, beams, d), dtype=np.float32))
     kt = round_bf16(rng.standard_normal((1, h, d, frames), dtype=np.float32))
     vx = round_bf16(rng.standard_normal((1, h, frames, d), dtype=np.float32))
-    qd, kd, vd = _dev(qx, bf, gpu), _dev(kt, bf, gpu), _dev(vx, bf, gpu)
-    ox = torch.empty(1, h, beams, d, device=gpu)
-    plan = fa.plan(qd, kd, vd, ox, k_transposed=True, scale=scale)
-    print("cross plan", plan)
-    assert plan["kernel"] == "decode" and plan["splits"] > 1
-    assert fa.attention(qd, kd, vd, k_transposed=True, scale=scale, out=ox) is not None
     want = oracle.attend_general(qx, kt, vx, k_transposed=True, scale=scale)
-    err = max_abs(ox.cpu().numpy(), want)
-    print(f"beam-5 cross-attention: {err:.3e}")
-    assert err < TOL_BF16
+    # the cache's K either transposed (the reference's layout) or as rows (the bench's)
+    for k_transposed in (True, False):
+        kk = kt if k_transposed else np.ascontiguousarray(np.swapaxes(kt, 2, 3))
+        qd, kd, vd = _dev(qx, bf, gpu), _dev(kk, bf, gpu), _dev(vx, bf, gpu)
+        ox = torch.empty(1, h, beams, d, device=gpu)
+        plan = fa.plan(qd, kd, vd, ox, k_transposed=k_transposed, scale=scale)
+        print("cross plan", plan)
+        assert plan["kernel"] == "decode" and plan["splits"] > 1
+        assert fa.attention(qd, kd, vd, k_transposed=k_transposed, scale=scale, out=ox) is not None
+        err = max_abs(ox.cpu().numpy(), want)
+        print(f"beam-5 cross-attention (k_transposed={k_transposed}): {err:.3e}")
+        assert err < TOL_BF16
