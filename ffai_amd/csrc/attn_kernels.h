@@ -105,6 +105,9 @@ hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int 
 // with p.n_split > 1 the unit's last workgroup merges the splits (p.counters zeroed).
 hipError_t launch_decode(const DecodeParams& p, int mode, int out_dtype, int head_dim,
                          bool k_transposed, int waves, hipStream_t stream);
+// f16 inputs (decode_f16.hip), called by launch_decode.
+hipError_t launch_decode_f16(const DecodeParams& p, int out_dtype, int head_dim,
+                             bool k_transposed, int waves, hipStream_t stream);
 
 // Error and device helpers of the C ABI (attn_api.cpp), for the other entry-point units.
 int api_fail(int code, const char* msg);  // records msg for ffai_attn_last_error, returns code

@@ -1,49 +1,14 @@
-// Instantiations and launch of the decode kernel (bf16 and f16; head_dim 64 with 1, 2, 4 or 8
-// waves, head_dim 128 with 1, 2 or 4; K given transposed or as rows; f32 or same-type output).
-// Split units merge inside the same launch (the unit's last workgroup), so a call is one launch.
-#include "decode_kernels.cuh"
+// bf16 instantiations of the decode kernel, and the dispatch on the input type (the f16 ones are
+// in decode_f16.hip: two translation units compile in parallel).
+#include "decode_launch.cuh"
 
 namespace ffai {
-namespace {
-
-template <int MODE, int OUTT, int D, bool KT, int NWD>
-hipError_t launch_dec(const DecodeParams& p, hipStream_t s) {
-  const dim3 grid((unsigned)p.n_split, (unsigned)p.Hkv, (unsigned)p.B);  // (split, kv-head, batch)
-  hipLaunchKernelGGL((decode_kernel<MODE, OUTT, D, KT, NWD>), grid, dim3(NWD * 64), 0, s, p);
-  return hipGetLastError();
-}
-
-template <int MODE, int OUTT, int D, bool KT>
-hipError_t pick_waves(const DecodeParams& p, int waves, hipStream_t s) {
-  if (waves == 1) return launch_dec<MODE, OUTT, D, KT, 1>(p, s);
-  if (waves == 2) return launch_dec<MODE, OUTT, D, KT, 2>(p, s);
-  if (waves == 4) return launch_dec<MODE, OUTT, D, KT, 4>(p, s);
-  if constexpr (D == 64) {
-    if (waves == 8) return launch_dec<MODE, OUTT, D, KT, 8>(p, s);
-  }
-  return hipErrorInvalidValue;
-}
-
-template <int MODE, int OUTT>
-hipError_t pick(const DecodeParams& p, int d, bool kt, int waves, hipStream_t s) {
-  if (d == 64) return kt ? pick_waves<MODE, OUTT, 64, true>(p, waves, s)
-                         : pick_waves<MODE, OUTT, 64, false>(p, waves, s);
-  if (d == 128) return kt ? pick_waves<MODE, OUTT, 128, true>(p, waves, s)
-                          : pick_waves<MODE, OUTT, 128, false>(p, waves, s);
-  return hipErrorInvalidValue;
-}
-
-}  // namespace
 
 hipError_t launch_decode(const DecodeParams& p, int mode, int out_dtype, int head_dim,
                          bool k_transposed, int waves, hipStream_t stream) {
-  if (mode == kBF16) {
-    if (out_dtype == kF32) return pick<kBF16, kF32>(p, head_dim, k_transposed, waves, stream);
-    if (out_dtype == kBF16) return pick<kBF16, kBF16>(p, head_dim, k_transposed, waves, stream);
-  } else if (mode == kF16) {
-    if (out_dtype == kF32) return pick<kF16, kF32>(p, head_dim, k_transposed, waves, stream);
-    if (out_dtype == kF16) return pick<kF16, kF16>(p, head_dim, k_transposed, waves, stream);
-  }
+  if (mode == kBF16)
+    return launch_decode_mode<kBF16>(p, out_dtype, head_dim, k_transposed, waves, stream);
+  if (mode == kF16) return launch_decode_f16(p, out_dtype, head_dim, k_transposed, waves, stream);
   return hipErrorInvalidValue;
 }
 

@@ -36,7 +36,8 @@ __device__ __forceinline__ void store_row_chunk(const DecodeParams& p, int b, in
   st4<OUTT, true>(op, acc * inv);
 }
 
-template <int MODE, int OUTT, int D, bool KT, int NWD>
+// NC: 16-column blocks of query rows (1 for units of at most 16 rows, 2 for up to 32).
+template <int MODE, int OUTT, int D, bool KT, int NWD, int NC>
 __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   static_assert(MODE == kBF16 || MODE == kF16, "decode kernel reads 16-bit Q, K and V");
   // Per-wave LDS: one K tile ([key][d] or [d][key]) and one V tile ([key][d]), 16-bit, rows
@@ -70,12 +71,19 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   // compiler does not wait on one branch's loads before another's (it did: the register-staging
   // loads of the tail path made it await the Q loads before issuing any K/V DMA)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 5;
-  const int n32 = lane & 31;  // this lane's query row of the unit (MFMA column)
+  const int q4 = lane >> 4;   // lane group: contraction elements 8 q4 .., accumulator rows 4 q4 ..
+  const int n16 = lane & 15;  // this lane's column in each 16-column block
   const int R = p.group * p.Tq;
-  const int rn = min(n32, R - 1);
-  const int t_row = rn % p.Tq;
-  const int h_row = hk * p.group + rn / p.Tq;
+  // the unit's query row of column c (block c / 16): n = 16 c + n16; columns past R repeat row
+  // R - 1 (each column's scores, weights and sums stay in that column, and only the first R
+  // are read back)
+  int t_row[NC], h_row[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int rn = min(16 * c + n16, R - 1);
+    t_row[c] = rn % p.Tq;
+    h_row[c] = hk * p.group + rn / p.Tq;
+  }
 
   int kv_end = p.Tk;
   if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
@@ -87,18 +95,27 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   const int t_end = min(n_tiles, t_begin + p.tiles_per_split);
   const int iters = t_end > t_begin ? (t_end - t_begin + NWD - 1) / NWD : 0;
   const float sl2 = p.scale_log2;
-  const int lim = p.causal ? min(kv_end - 1, p.q_offset + t_row) : kv_end - 1;
+  int lim[NC];  // the last key column block c's row may see
+#pragma unroll
+  for (int c = 0; c < NC; ++c) lim[c] = p.causal ? min(kv_end - 1, p.q_offset + t_row[c]) : kv_end - 1;
 
   const uint16_t* kp = reinterpret_cast<const uint16_t*>(p.k) + b * p.k_sb + hk * p.k_sh;
   const uint16_t* vp = reinterpret_cast<const uint16_t*>(p.v) + b * p.v_sb + hk * p.v_sh;
 
-  f32x16 oacc[D / 32];
+  // O^T per column block, 16 d per accumulator: oacc[c][db][r] <-> d = 16 db + 4 q4 + r of
+  // column 16 c + n16
+  f32x4 oacc[NC][D / 16];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt)
+  for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  float m_s = kNegInf;  // running max, scaled log2 units (same in lane and lane ^ 32)
-  float l_run = 0.f;    // this lane's half of the running sum
+    for (int db = 0; db < D / 16; ++db) oacc[c][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_s[NC], l_run[NC];  // running max (scaled log2 units, the same in all four lane
+                             // groups) and this lane group's part of the running sum
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    m_s[c] = kNegInf;
+    l_run[c] = 0.f;
+  }
 
   uint16_t* kl = lds + wave * WBUF;
   uint16_t* vl = kl + KBUF;
@@ -106,9 +123,9 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   auto swz_kt = [](int r, int c) { return c ^ (4 * ((r >> 1) & 1)); };
   auto swz_v = [](int r, int c) { return D == 64 ? c ^ (4 * ((r >> 1) & 1)) : c ^ (4 * (r & 3)); };
   auto swz_kr = [](int r, int c) { return D == 64 ? c ^ ((r >> 1) & 7) : c ^ (r & 15); };
-  const int jt = lane & 15;
-  const int tr_row = jt >> 2, tr_col = 4 * (jt & 3);
-  const int half16 = 16 * ((lane >> 4) & 1);
+  // transposing LDS reads: in each 16-lane group, lane j reads 4 elements of row r0 + j / 4 at
+  // column c0 + 4 (j % 4), and then holds column c0 + j of rows r0 .. r0 + 3
+  const int tr_row = n16 >> 2, tr_col = 4 * (n16 & 3);
 
   // ---- staging (the host launches this kernel only for operands that admit its vector
   //      accesses). Rows of K and V: 16-byte units, the key index clamped to the last valid key
@@ -124,7 +141,10 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   constexpr int KCH = KT ? BN / 8 : D / 8, KRB = 64 / KCH;  // K: chunks per row, rows per block
   constexpr int VCH = D / 8, VRB = 64 / VCH;
   const int kr = lane / KCH, kpc = lane % KCH, vr = lane / VCH, vpc = lane % VCH;
-  auto dma_tile = [&](int it) {
+  // `valid`: the tile's keys before the end of the cache (wave-uniform). Blocks of K or V rows
+  // that hold none of them are not read: their LDS rows keep stale values, whose keys are masked
+  // and whose V rows are cleared once the DMA has landed (ragged tails of per-beam caches).
+  auto dma_tile = [&](int it, int valid) {
     const int64_t kb = (int64_t)it * BN;
     const uint32_t kla = lds_addr(kl), vla = lds_addr(vl);
     const char* kbase = reinterpret_cast<const char*>(kp + (KT ? kb : kb * p.k_st));
@@ -134,13 +154,15 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       const int r = j * KRB + kr;
       const uint32_t off =
           (uint32_t)(2 * (kr * p.k_st + 8 * (KT ? swz_kt(r, kpc) : swz_kr(r, kpc))));
-      lds_dma16_sbase<true>(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
+      if (KT || j * KRB < valid)
+        lds_dma16_sbase<true>(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
     }
 #pragma unroll
     for (int j = 0; j < VBUF / 512; ++j) {
       const int r = j * VRB + vr;
       const uint32_t off = (uint32_t)(2 * (vr * p.v_st + 8 * swz_v(r, vpc)));
-      lds_dma16_sbase<true>(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
+      if (j * VRB < valid)
+        lds_dma16_sbase<true>(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
     }
   };
   // The operand's last tile, when it has at least 8 keys but fewer than 64 (cross-attention over
@@ -277,7 +299,7 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   // Issue tile `it`'s loads (by DMA, or through registers for a short end).
   auto issue_tile = [&](int it) {
     const int kb = it * BN;
-    if (kb + BN <= kv_end || tail_dma_of(kb)) dma_tile(it);
+    if (kb + BN <= kv_end || tail_dma_of(kb)) dma_tile(it, min(BN, kv_end - kb));
     else if (end_dma_of(kb)) dma_tile_clamped(it);
     else stage_tile(it);
     if (patch_end_of(kb)) patch_kt_load();
@@ -287,16 +309,15 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   // the DMA wait for the Q loads: registers it reuses were load targets on the register-staging
   // path, and one in-order counter covers both.)
   if (iters > 0 && t_begin + wave < t_end) issue_tile(t_begin + wave);
-  // ---- Q fragments: B operand of S^T, step s: d = 16s + 8g .. +7 of row rn. Issued after the
-  //      wave's first K/V loads (below). Columns past the unit's R rows repeat row R - 1: each
-  //      column's scores, weights and sums stay in that column, and only the first R are ever
-  //      read back.
-  u32x4 qf[D / 16];
-  {
-    const uint16_t* qr = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_sb + h_row * p.q_sh +
-                         (int64_t)t_row * p.q_st;
+  // ---- Q fragments (issued after the wave's first K/V loads): B operand of S^T, block c,
+  //      contraction chunk h: d = 32 h + 8 q4 .. +7 of column 16 c + n16's row
+  u32x4 qf[NC][D / 32];
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) qf[s] = ld16(qr + 16 * s + 8 * g);
+  for (int c = 0; c < NC; ++c) {
+    const uint16_t* qr = reinterpret_cast<const uint16_t*>(p.q) + b * p.q_sb +
+                         h_row[c] * p.q_sh + (int64_t)t_row[c] * p.q_st;
+#pragma unroll
+    for (int h = 0; h < D / 32; ++h) qf[c][h] = ld16(qr + 32 * h + 8 * q4);
   }
 
 #pragma unroll 1
@@ -320,64 +341,67 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
         *reinterpret_cast<u32x4*>(&vl[8 * u]) = u32x4{0u, 0u, 0u, 0u};
     }
 
-    // ---- S^T for the tile's two 32-key subtiles: sacc[st][r] <-> key kb + 32st + 8(r/4) +
-    //      4g + r%4 of row n32
-    f32x16 sacc[2];
+    // ---- S^T per 16-key block kb4 of the tile, on 16x16x32 MFMA:
+    //      sacc[c][kb4][r] <-> key kb + 16 kb4 + 4 q4 + r of column 16 c + n16
+    f32x4 sacc[NC][4];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int kb4 = 0; kb4 < 4; ++kb4) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[st][r] = 0.f;
+      for (int c = 0; c < NC; ++c) sacc[c][kb4] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) {
+      for (int h = 0; h < D / 32; ++h) {
+        // A: key 16 kb4 + n16, d = 32 h + 8 q4 .. +7
         u32x4 a;
         if constexpr (KT) {
-          // rows r and r + 4 share the chunk permutation (it depends on bit 1 of the row)
-          const int r = 16 * s + 8 * g + tr_row, col = 32 * st + half16 + tr_col;
+          // K^T [d][key]: rows r and r + 4 share the chunk permutation (bit 1 of the row)
+          const int r = 32 * h + 8 * q4 + tr_row, col = 16 * kb4 + tr_col;
           const uint16_t* base = &kl[r * KTROW + 8 * swz_kt(r, col >> 3) + (col & 7)];
           const u32x2 lo = lds_tr(base), hi = lds_tr(base + 4 * KTROW);
           a = u32x4{lo.x, lo.y, hi.x, hi.y};
         } else {
-          const int r = 32 * st + n32;
-          a = *reinterpret_cast<const u32x4*>(&kl[r * KROW + 8 * swz_kr(r, 2 * s + g)]);
+          const int r = 16 * kb4 + n16;
+          a = *reinterpret_cast<const u32x4*>(&kl[r * KROW + 8 * swz_kr(r, 4 * h + q4)]);
         }
-        sacc[st] = mfma16<MODE>(a, qf[s], sacc[st]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) sacc[c][kb4] = mfma16x16<MODE>(a, qf[c][h], sacc[c][kb4]);
       }
     }
     // ---- mask (only tiles that reach past a row's last visible key: the ragged end, or the
     //      causal diagonal of the unit's first row), max, rescale, weights
     if (kb + BN > kv_end || (p.causal && kb + BN - 1 > p.q_offset)) {  // wave-uniform
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * st + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key > lim) sacc[st][r] = kNegInf;
-        }
+        for (int kb4 = 0; kb4 < 4; ++kb4)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kb + 16 * kb4 + 4 * q4 + r > lim[c]) sacc[c][kb4][r] = kNegInf;
     }
-    float mx = kNegInf;
+    // P per column block and 32-key chunk ch, the B operand of O^T += V^T P^T: lane group q4's
+    // contraction slots e hold keys 32 ch + 4 q4 + e (e < 4) and 32 ch + 16 + 4 q4 + e - 4
+    // (blocks 2 ch and 2 ch + 1 of S^T as they lie in the lane); V is read in the same order
+    u32x4 pf[NC][2];
+    float corr[NC];
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int c = 0; c < NC; ++c) {
+      float mx = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(sacc[st][r], sacc[st][r + 1]));
-    const float m_new = fmaxf(m_s, partner_max(mx) * sl2);
-    const float corr = (m_new == kNegInf) ? 1.f : fast_exp2(m_s - m_new);
-    m_s = m_new;
-    const float mc = (m_new == kNegInf) ? 0.f : m_new;
-    if (i > 0) {  // the first tile finds the accumulator still zero (wave-uniform)
+      for (int kb4 = 0; kb4 < 4; ++kb4)
+        mx = fmaxf(mx, fmaxf(fmaxf(sacc[c][kb4][0], sacc[c][kb4][1]),
+                             fmaxf(sacc[c][kb4][2], sacc[c][kb4][3])));
+      const float m_new = fmaxf(m_s[c], quad_max(mx) * sl2);
+      corr[c] = (m_new == kNegInf) ? 1.f : fast_exp2(m_s[c] - m_new);
+      m_s[c] = m_new;
+      const float mc = (m_new == kNegInf) ? 0.f : m_new;
+      float rs = 0.f;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= corr;
-    }
-    u32x4 pf[4];
-    float rs = 0.f;
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
+      for (int ch = 0; ch < 2; ++ch) {
         uint32_t w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float e0 = fast_exp2(__builtin_fmaf(sacc[st][8 * h2 + 2 * k], sl2, -mc));
-          const float e1 = fast_exp2(__builtin_fmaf(sacc[st][8 * h2 + 2 * k + 1], sl2, -mc));
+          const f32x4& sv = sacc[c][2 * ch + (k >> 1)];
+          const float e0 = fast_exp2(__builtin_fmaf(sv[2 * (k & 1)], sl2, -mc));
+          const float e1 = fast_exp2(__builtin_fmaf(sv[2 * (k & 1) + 1], sl2, -mc));
           const uint32_t pk = pack2<MODE>(e0, e1);
           w[k] = pk;
           if constexpr (MODE == kBF16) {
@@ -388,19 +412,28 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
                                         f16x2{(_Float16)1.f, (_Float16)1.f}, rs, false);
           }
         }
-        pf[2 * st + h2] = u32x4{w[0], w[1], w[2], w[3]};
+        pf[c][ch] = u32x4{w[0], w[1], w[2], w[3]};
       }
-    l_run = __builtin_fmaf(l_run, corr, rs);
-    // ---- O^T += V^T P^T: 16-key chunk t, A(d = 32dt + n32, keys 16t + 4g + e, 16t + 8 + 4g + e)
+      l_run[c] = __builtin_fmaf(l_run[c], corr[c], rs);
+    }
+    if (i > 0) {  // the first tile finds the accumulators still zero (wave-uniform)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
-        // rows r and r + 8 share the chunk permutation
-        const int r = 16 * t + 4 * g + tr_row, col = 32 * dt + half16 + tr_col;
+        for (int db = 0; db < D / 16; ++db) oacc[c][db] *= corr[c];
+    }
+    // ---- O^T += V^T P^T: A(d = 16 db + n16, slot e) = V(key of slot e, d), read transposed from
+    //      the [key][d] tile: rows r and r + 16 share the chunk permutation
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        const int r = 32 * ch + 4 * q4 + tr_row, col = 16 * db + tr_col;
         const uint16_t* base = &vl[r * VROW + 8 * swz_v(r, col >> 3) + (col & 7)];
-        const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 8 * VROW);
-        oacc[dt] = mfma16<MODE>(u32x4{a0.x, a0.y, a1.x, a1.y}, pf[t], oacc[dt]);
+        const u32x2 a0 = lds_tr(base), a1 = lds_tr(base + 16 * VROW);
+        const u32x4 a = {a0.x, a0.y, a1.x, a1.y};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) oacc[c][db] = mfma16x16<MODE>(a, pf[c][ch], oacc[c][db]);
       }
   }
 
@@ -409,18 +442,19 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   float* mbase = reinterpret_cast<float*>(lds);
   {
     float* mb = mbase + wave * (WBUF / 2);
-    const float l_tot = partner_sum(l_run);  // the whole wave takes part (a lane swap)
-    // only the unit's R rows are read back: the other columns' lanes write nothing
-    if (n32 < R) {
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+    for (int c = 0; c < NC; ++c) {
+      const float l_tot = quad_sum(l_run[c]);  // the whole wave takes part (lane swaps)
+      const int n = 16 * c + n16;
+      // only the unit's R rows are read back: the other columns' lanes write nothing
+      if (n < R) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<f32x4*>(&mb[n32 * OROW + 32 * dt + 8 * r + 4 * g]) =
-              f32x4{oacc[dt][4 * r], oacc[dt][4 * r + 1], oacc[dt][4 * r + 2], oacc[dt][4 * r + 3]};
-      if (g == 0) {
-        mb[32 * OROW + n32] = m_s;
-        mb[32 * OROW + 32 + n32] = l_tot;
+        for (int db = 0; db < D / 16; ++db)
+          *reinterpret_cast<f32x4*>(&mb[n * OROW + 16 * db + 4 * q4]) = oacc[c][db];
+        if (q4 == 0) {
+          mb[32 * OROW + n] = m_s[c];
+          mb[32 * OROW + 32 + n] = l_tot;
+        }
       }
     }
   }
