@@ -11,6 +11,7 @@ disabled for all device code.
 
 from __future__ import annotations
 
+import json
 import os
 import shutil
 import subprocess
@@ -50,16 +51,47 @@ def flags() -> list[str]:
     ]
 
 
-def _run(cmd: list[str], verbose: bool) -> None:
+# Per-kernel register, scratch and occupancy figures the compiler reports, written at every
+# build (kernel name -> {"vgprs", "agprs", "scratch", "occupancy", "vgpr_spill", "sgpr_spill"}).
+# The fused kernels sit at their register budget, where a small change of the code can make the
+# compiler spill to scratch: correct results, several times slower. A CPU test reads this file.
+RESOURCES_PATH = os.path.join(BUILD_DIR, "resource_usage.json")
+_REMARK = "-Rpass-analysis=kernel-resource-usage"
+_FIELDS = {"VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch",
+           "Occupancy [waves/SIMD]": "occupancy", "VGPRs Spill": "vgpr_spill",
+           "SGPRs Spill": "sgpr_spill"}
+
+
+def _resources(stderr: str) -> dict:
+    """The compiler's kernel-resource-usage remarks of one compile, by kernel."""
+    out, cur = {}, None
+    for line in stderr.splitlines():
+        if "remark:" not in line or _REMARK not in line:
+            continue
+        body = line.split("remark:", 1)[1].replace(f"[{_REMARK}]", "").strip()
+        key, _, val = body.partition(":")
+        key, val = key.strip(), val.strip()
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None and key in _FIELDS:
+            try:
+                cur[_FIELDS[key]] = int(val)
+            except ValueError:
+                pass
+    return out
+
+
+def _run(cmd: list[str], verbose: bool) -> dict:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l and "remark:" not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+    return _resources(res.stderr)
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> str:
@@ -72,10 +104,14 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     for src in SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
         objs.append(obj)
-        cmds.append([cc] + flags() + ["-c", "-x", "hip", src, "-o", obj])
+        cmds.append([cc] + flags() + [_REMARK, "-c", "-x", "hip", src, "-o", obj])
     jobs = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 8)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(lambda c: _run(c, verbose), cmds))
+        usage = {}
+        for r in ex.map(lambda c: _run(c, verbose), cmds):
+            usage.update(r)
+    with open(RESOURCES_PATH, "w") as f:
+        json.dump(usage, f, indent=0, sort_keys=True)
     tmp = LIB_PATH + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + LIBS, verbose)
     os.replace(tmp, LIB_PATH)

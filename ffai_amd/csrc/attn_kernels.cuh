@@ -81,14 +81,13 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   __shared__ __attribute__((aligned(16))) LT v_lds[NBUF * VBUF];
 
   // ---- which work (an item, or one piece of a split item) this workgroup computes
-  const int hw = wg_id_x();
+  const int hw = blockIdx.x;
   int work;
   if (hw < p.sec1_wgs) {
     work = p.xcd_remap ? (hw & 7) * (p.sec1_wgs >> 3) + (hw >> 3) : hw;
     if (work >= p.sec1_work) return;
   } else {
-    // the second section: the launch rounds its works up to whole XCD rounds
-    const int x = hw - p.sec1_wgs, n = (p.n_work - p.sec1_work + 7) / 8 * 8;
+    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;  // n: a multiple of 8
     work = p.sec1_work + (p.xcd_remap ? (x & 7) * (n >> 3) + (x >> 3) : x);
     if (work >= p.n_work) return;
   }
@@ -115,7 +114,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   const int b = bh / p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
 
-  const int tid = item_id();
+  const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps q0 scalar
   const int g = lane >> 5;    // lane group: which half of each MFMA contraction step

@@ -14,16 +14,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void probe_empty_kernel() {}
 
 // Workgroup w reads its contiguous share of the 16-byte chunks, each thread issuing up to 16
-// independent loads before it uses any (as the decode kernel has its whole share in flight), and
-// thread 0 writes the workgroup's XOR of them (it keeps the loads alive).
+// independent loads before it uses any (as the decode kernel has its whole share in flight).
+// Nothing is reduced across threads: a thread stores only if its XOR of the data equals a value
+// the data never produces (all-zero input), which keeps the loads alive without adding a serial
+// tail to the read.
 __global__ __launch_bounds__(256) void probe_read_kernel(const u32x4* src, int64_t chunks,
-                                                         float* out) {
+                                                         int64_t per, float* out) {
   constexpr int kBatch = 16;
-  const int64_t per = (chunks + gridDim.x - 1) / gridDim.x;
-  const int64_t begin = (int64_t)blockIdx.x * per;
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wg = (int)__builtin_amdgcn_workgroup_id_x();
+  const int64_t begin = (int64_t)wg * per;
   const int64_t end = begin + per < chunks ? begin + per : chunks;
   uint32_t acc = 0;
-  for (int64_t i0 = begin + threadIdx.x; i0 < end; i0 += 256 * kBatch) {
+  for (int64_t i0 = begin + tid; i0 < end; i0 += 256 * kBatch) {
     u32x4 x[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
@@ -34,14 +37,7 @@ __global__ __launch_bounds__(256) void probe_read_kernel(const u32x4* src, int64
     for (int j = 0; j < kBatch; ++j)
       if (i0 + (int64_t)j * 256 < end) acc ^= x[j][0] ^ x[j][1] ^ x[j][2] ^ x[j][3];
   }
-  __shared__ uint32_t red[256];
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t s = 0;
-    for (int t = 0; t < 256; ++t) s ^= red[t];
-    out[blockIdx.x] = (float)s;
-  }
+  if (acc == 0x9e3779b9u) out[wg] = (float)acc;
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -99,9 +95,10 @@ int ffai_probe_read(const void* src, size_t bytes, float* out, int workgroups, v
     return ffai::api_fail(FFAI_ERR_INVALID,
                           "src and out must be set, bytes a positive multiple of 16, src 16-byte "
                           "aligned, workgroups >= 1");
+  const int64_t chunks = (int64_t)(bytes / 16);
   hipLaunchKernelGGL(probe_read_kernel, dim3((unsigned)workgroups), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
-                     (int64_t)(bytes / 16), out);
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src), chunks,
+                     (chunks + workgroups - 1) / workgroups, out);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? FFAI_OK : ffai::api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
 }
