@@ -180,7 +180,9 @@ def test_beam5_decode_step_shapes(gpu):
     kt = round_bf16(rng.standard_normal((1, h, d, frames), dtype=np.float32))
     vx = round_bf16(rng.standard_normal((1, h, frames, d), dtype=np.float32))
     want = oracle.attend_general(qx, kt, vx, k_transposed=True, scale=scale)
-    # the cache's K either transposed (the reference's layout) or as rows (the bench's)
+    # the cache's K either transposed (the reference's layout) or as rows (the bench's); both
+    # layouts feed the MFMAs the same operands in the same order, so their outputs are equal
+    outs = []
     for k_transposed in (True, False):
         kk = kt if k_transposed else np.ascontiguousarray(np.swapaxes(kt, 2, 3))
         qd, kd, vd = _dev(qx, bf, gpu), _dev(kk, bf, gpu), _dev(vx, bf, gpu)
@@ -192,3 +194,5 @@ def test_beam5_decode_step_shapes(gpu):
         err = max_abs(ox.cpu().numpy(), want)
         print(f"beam-5 cross-attention (k_transposed={k_transposed}): {err:.3e}")
         assert err < TOL_BF16
+        outs.append(ox)
+    assert torch.equal(outs[0], outs[1])
