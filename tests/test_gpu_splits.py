@@ -288,3 +288,60 @@ def test_seeded_layouts_against_the_oracle(gpu, split_override, case):
     print(f"case {case}: plan {plan}, err {err:.3e}")
     assert err < (TOL_F32 if dtype == "f32" else TOL_BF16)
     assert _counters_zero(ws)
+
+
+def _broad_cases(seed, n):
+    """Random shapes up to whisper-window size: 1-1700 keys, 1-1600 queries (a quarter of them
+    decode-sized, at most 32), ragged or not, causal with the queries at the end of the keys,
+    grouped heads, head_dim 64/128, K rows or transposed, f32 or 16-bit outputs, and the
+    planner's layout or a forced split."""
+    rng = np.random.default_rng(seed)
+    for i in range(n):
+        d = int(rng.choice([64, 128]))
+        dtype = str(rng.choice(["bf16", "f16", "f32"] if d == 64 else ["bf16", "f16"]))
+        hkv = int(rng.integers(1, 4))
+        hq = hkv * int(rng.integers(1, 5)) if dtype != "f32" else hkv
+        b = int(rng.integers(1, 4))
+        causal = bool(rng.integers(0, 2)) and dtype != "f32"
+        tk = int(rng.integers(1, 1700))
+        tq = int(rng.integers(1, 33)) if rng.integers(0, 4) == 0 else int(rng.integers(1, 1600))
+        if causal:
+            tq = min(tq, tk)
+        ragged = bool(rng.integers(0, 2))
+        items = int(rng.choice([0, 0, 0, -1, 1, 3, 7]))
+        pieces = int(rng.integers(2, 6))
+        kt = bool(rng.integers(0, 2))
+        out16 = bool(rng.integers(0, 2)) and dtype != "f32"
+        yield i, b, hq, hkv, tq, tk, d, dtype, causal, ragged, items, pieces, kt, out16
+
+
+def test_broad_seeded_sweep_against_the_oracle(gpu, split_override):
+    """400 seeded random calls (see _broad_cases) against the oracle, one process: every output
+    within tolerance and every split counter zero again afterwards."""
+    worst, kernels = {}, {}
+    for case in _broad_cases(7, 400):
+        i, b, hq, hkv, tq, tk, d, dtype, causal, ragged, items, pieces, kt, out16 = case
+        rng = np.random.default_rng(7000 + i)
+        tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+        rnd = {"bf16": round_bf16, "f16": round_f16, "f32": lambda x: x}[dtype]
+        q = rnd(randn(rng, (b, hq, tq, d)))
+        k = rnd(randn(rng, (b, hkv, d, tk) if kt else (b, hkv, tk, d)))
+        v = rnd(randn(rng, (b, hkv, tk, d)))
+        lens = rng.integers(0, tk + 1, size=b).astype(np.int32) if ragged else None
+        split_override(items, pieces) if items else split_override(0, 0)
+        q_offset = tk - tq if causal else 0
+        kw = dict(scale=d ** -0.5, causal=causal, q_offset=q_offset, k_transposed=kt)
+        if lens is not None:
+            kw["kv_lens"] = torch.from_numpy(lens).to(gpu)
+        out, plan, ws = _run(_dev(q, tdt, gpu), _dev(k, tdt, gpu), _dev(v, tdt, gpu),
+                             out_dtype=tdt if out16 else torch.float32, **kw)
+        want = oracle.attend_general(q, k, v, k_transposed=kt, scale=kw["scale"], causal=causal,
+                                     q_offset=q_offset, kv_lens=lens)
+        err = max_abs(out.float().cpu().numpy(), want)
+        tag = dtype + ("/out16" if out16 else "")
+        worst[tag] = max(worst.get(tag, 0.0), err)
+        kernels[plan["kernel"]] = kernels.get(plan["kernel"], 0) + 1
+        assert err < (TOL_F32 if dtype == "f32" else TOL_BF16), (case, plan, err)
+        assert _counters_zero(ws), (case, plan)
+    print("kernels", kernels, "worst", {t: f"{e:.2e}" for t, e in worst.items()})
+    assert set(kernels) == {"fwd", "decode"}
