@@ -59,12 +59,13 @@ def test_append_matches_concatenation(gpu, src, dst):
         np.testing.assert_array_equal(v[s, :, :n], want_v)
 
 
-@pytest.mark.parametrize("t_new", [1, 200])
+@pytest.mark.parametrize("t_new", [1, 20, 200])
 def test_append_clamps_lengths_out_of_range(gpu, t_new):
     """A corrupt length (negative, or above capacity) is clamped into [0, capacity] before the
     append, as the gather clamps it: rows of a slot at -1 land from position 0, a slot past
     capacity takes nothing, and no row lands outside the slot's cache. One row (one workgroup
-    per slot, length advanced in the same launch) and 200 rows (several workgroups per slot,
+    per slot, length advanced in the same launch), 20 rows (640 units: still one workgroup,
+    three units a thread) and 200 rows (one unit a thread over several workgroups per slot,
     separate length update)."""
     rng = np.random.default_rng(17)
     slots, heads, d, cap = 3, 4, 64, 256
