@@ -266,13 +266,16 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // four-wave grids (two workgroups per CU) of fewer items than CUs fill the 512 slots:
   // whisper-tiny f32 50.5 us in 6 pieces against 56.4 in 3, 66.2 in 4 (288 works: a second
   // round) and 77.9 in 2; up to 1024 items they aim at ~4096 waves (300 items: 183 us in 4
-  // pieces against 236 whole, 197 in 2, 211 in 8). One-wave grids (prompt steps, f32 and
-  // misaligned decode) keep about 512 workgroups: the cross-attention of 228 tokens, 128 items,
-  // 19.3 us in 4 pieces against 22.3 in 2 and 26.2 in 8; f32 decode over 1500 keys, 6 heads:
-  // 25.9 us in 24 pieces, 32.7 in 8, 193 whole; 80 items: 55.8 in 7, 73.9 in 4, 86.8 in 24.
+  // pieces against 236 whole, 197 in 2, 211 in 8). One-wave 16-bit grids (prompt steps,
+  // misaligned decode) fill at most the 768 slots of three workgroups per CU (48 KB of LDS
+  // each): the cross-attention of 228 tokens, 128 items, 14.6 us in 6 pieces against 15.4 in 5,
+  // 15.7 in 4 and 19.2 in 7 (896 workgroups: a second round). One-wave f32 grids (two per CU)
+  // keep about 512 workgroups: f32 decode over 1500 keys, 6 heads: 25.9 us in 24 pieces, 32.7
+  // in 8, 193 whole; 80 items: 55.8 in 7, 73.9 in 4, 86.8 in 24.
   int64_t want = 1;
   if (p.variant == ffai::kWave1) {
-    if (items < 512) want = std::min<int64_t>(f32 ? 24 : ffai::kMaxFwdSplits, (512 + items - 1) / items);
+    if (f32 && items < 512) want = std::min<int64_t>(24, (512 + items - 1) / items);
+    else if (!f32 && items < 768) want = std::min<int64_t>(ffai::kMaxFwdSplits, 768 / items);
   } else if (items < 256) {
     want = f32 ? 512 / items : std::max<int64_t>(1, std::min<int64_t>(3, 256 / items));
   } else if (f32 && items < 1024) {

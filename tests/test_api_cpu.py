@@ -411,9 +411,10 @@ def _plan(lib, *args, causal=0):
     # a whisper-large-v3 window (encoder block): 240 items, whole
     ((L.BF16, L.BF16, L.BF16, 1, 20, 20, 1500, 1500, 64, L.K_ROWS), 0,
      [0, 1, 1, 24, 240], [240, 0, 0]),
-    # prompt step cross-attention: 228 tokens x 16 heads, one-wave items in 4 pieces
+    # prompt step cross-attention: 228 tokens x 16 heads, one-wave items in 6 pieces (768
+    # workgroups, three per CU)
     ((L.BF16, L.BF16, L.F32, 1, 16, 16, 228, 1500, 64, L.K_TRANSPOSED), 0,
-     [0, 0, 4, 6, 512], [128, 0, 128]),
+     [0, 0, 6, 4, 768], [128, 0, 128]),
     # beam-5 cross-attention: the decode kernel, 8 pieces of 3 tiles per head (128 workgroups)
     ((L.BF16, L.BF16, L.F32, 1, 16, 16, 5, 1500, 64, L.K_TRANSPOSED), 0,
      [1, 4, 8, 3, 128], [0, 0, 0]),
