@@ -443,3 +443,23 @@ def test_split_override_and_its_workspace(lib):
         assert L.get_fwd_split_override() == (0, 0)
     finally:
         L.set_fwd_split_override(*prev)
+
+
+def test_one_wave_grids_stay_within_one_round(lib):
+    """One-wave 16-bit grids (query runs under 256 rows) are split towards the 768 slots of three
+    workgroups per CU and never past them: a 769th workgroup would start a second round."""
+    n = 0
+    for tq in (33, 64, 100, 228):
+        for heads in (1, 2, 5, 16, 24):
+            for b in (1, 3):
+                for tk in (64, 700, 1500, 3000):
+                    for dt in (L.BF16, L.F16):
+                        info, _ = _plan(lib, dt, dt, L.F32, b, heads, heads, tq, tk, 64, L.K_ROWS)
+                        if info[0] != 0 or info[1] != 0:  # the fused kernel's one-wave shape only
+                            continue
+                        n += 1
+                        items = b * heads * ((tq + 31) // 32)
+                        assert info[4] <= max(768, items), (dt, b, heads, tq, tk, info)
+                        if items < 384 and tk >= 128:   # room for two pieces of a tile or more
+                            assert info[2] >= 2, (dt, b, heads, tq, tk, info)
+    assert n > 50
