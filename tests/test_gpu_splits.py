@@ -186,21 +186,31 @@ def test_one_workspace_across_split_layouts(gpu, split_override):
         assert _counters_zero(ws)
 
 
-def test_pieces_in_graph_replays(gpu, split_override):
+@pytest.mark.parametrize("layout", ["forced", "prompt_cross"])
+def test_pieces_in_graph_replays(gpu, split_override, layout):
     """A launch with split items captured in a HIP graph: every replay (with eager work and
     synchronisation between replays, new inputs copied in) equals the eager call on the same
     inputs bit for bit, and leaves the counters zero. Past the counters the workspace starts as
-    garbage (0xFF): partials are written before they are read."""
+    garbage (0xFF): partials are written before they are read. Layouts: 9 of 12 four-wave items
+    forced into 3 pieces (K transposed), and the planner's own layout for a prompt step's
+    cross-attention (228 queries x 16 heads over 1500 keys as rows: one-wave items in 6 pieces,
+    768 workgroups)."""
     rng = np.random.default_rng(77)
-    b, h, t, d = 2, 3, 700, 64
-    split_override(9, 3)
-    q = torch.empty(b, h, t, d, dtype=torch.bfloat16, device=gpu)
-    k = torch.empty(b, h, d, t, dtype=torch.bfloat16, device=gpu)
-    v = torch.empty(b, h, t, d, dtype=torch.bfloat16, device=gpu)
-    out = torch.empty(b, h, t, d, dtype=torch.float32, device=gpu)
-    args = dict(k_transposed=True, scale=0.125)
+    if layout == "forced":
+        b, h, tq, tk, d, kt = 2, 3, 700, 700, 64, True
+        split_override(9, 3)
+    else:
+        b, h, tq, tk, d, kt = 1, 16, 228, 1500, 64, False
+    q = torch.empty(b, h, tq, d, dtype=torch.bfloat16, device=gpu)
+    k = torch.empty((b, h, d, tk) if kt else (b, h, tk, d), dtype=torch.bfloat16, device=gpu)
+    v = torch.empty(b, h, tk, d, dtype=torch.bfloat16, device=gpu)
+    out = torch.empty(b, h, tq, d, dtype=torch.float32, device=gpu)
+    args = dict(k_transposed=kt, scale=0.125)
     plan = fa.plan(q, k, v, out, **args)
-    assert plan["splits"] == 3 and plan["split_items"][1] - plan["split_items"][0] == 9
+    if layout == "forced":
+        assert plan["splits"] == 3 and plan["split_items"][1] - plan["split_items"][0] == 9
+    else:
+        assert plan["splits"] == 6 and plan["workgroups"] == 768, plan
     nbytes = fa.workspace_bytes(q, k, v, out, **args)
     ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=gpu)
     ws[:COUNTER_BYTES].zero_()
@@ -219,7 +229,7 @@ def test_pieces_in_graph_replays(gpu, split_override):
         assert _counters_zero(ws)
     want = oracle.attend_general(inputs[0][0].float().cpu().numpy(),
                                  inputs[0][1].float().cpu().numpy(),
-                                 inputs[0][2].float().cpu().numpy(), k_transposed=True,
+                                 inputs[0][2].float().cpu().numpy(), k_transposed=kt,
                                  scale=0.125)
     assert max_abs(eager[0].cpu().numpy(), want) < TOL_BF16
     graph = torch.cuda.CUDAGraph()
