@@ -300,6 +300,17 @@ def test_seeded_layouts_against_the_oracle(gpu, split_override, case):
     assert _counters_zero(ws)
 
 
+def _dev_at(x, dtype, device, off):
+    """x on the device as a view starting `off` elements into a larger buffer."""
+    t = _dev(x, dtype, device)
+    if off == 0:
+        return t
+    buf = torch.empty(t.numel() + off, dtype=dtype, device=device)
+    view = buf[off:].view(t.shape)
+    view.copy_(t)
+    return view
+
+
 def _broad_cases(seed, n):
     """Random shapes up to whisper-window size: 1-1700 keys, 1-1600 queries (a quarter of them
     decode-sized, at most 32), ragged or not, causal with the queries at the end of the keys,
@@ -326,8 +337,9 @@ def _broad_cases(seed, n):
 
 
 def test_broad_seeded_sweep_against_the_oracle(gpu, split_override):
-    """400 seeded random calls (see _broad_cases) against the oracle, one process: every output
-    within tolerance and every split counter zero again afterwards."""
+    """400 seeded random calls (see _broad_cases) against the oracle, one process, every fourth
+    with misaligned inputs: every output within tolerance and every split counter zero again
+    afterwards."""
     worst, kernels = {}, {}
     for case in _broad_cases(7, 400):
         i, b, hq, hkv, tq, tk, d, dtype, causal, ragged, items, pieces, kt, out16 = case
@@ -343,7 +355,11 @@ def test_broad_seeded_sweep_against_the_oracle(gpu, split_override):
         kw = dict(scale=d ** -0.5, causal=causal, q_offset=q_offset, k_transposed=kt)
         if lens is not None:
             kw["kv_lens"] = torch.from_numpy(lens).to(gpu)
-        out, plan, ws = _run(_dev(q, tdt, gpu), _dev(k, tdt, gpu), _dev(v, tdt, gpu),
+        # every fourth call takes its inputs at 0-7 elements past 16-byte alignment (register
+        # staging instead of the DMA)
+        off = int(rng.integers(0, 8)) if i % 4 == 0 else 0
+        out, plan, ws = _run(_dev_at(q, tdt, gpu, off), _dev_at(k, tdt, gpu, off),
+                             _dev_at(v, tdt, gpu, off),
                              out_dtype=tdt if out16 else torch.float32, **kw)
         want = oracle.attend_general(q, k, v, k_transposed=kt, scale=kw["scale"], causal=causal,
                                      q_offset=q_offset, kv_lens=lens)
