@@ -259,7 +259,9 @@ def test_golden_vectors(path):
                                     kv_lens=z["lens"])
     else:
         pytest.fail(f"unknown fixture {name}")
-    assert max_abs(got, z["out"]) < 1e-6      # the oracle reproduces its committed output
+    # the oracle reproduces its committed output bit for bit (heads are independent, so the
+    # thread count does not change any sum's order)
+    assert np.array_equal(got, z["out"]), max_abs(got, z["out"])
     assert max_abs(z["out"], z["f64"]) < 3e-5  # which agrees with the closed form
 
 
