@@ -226,6 +226,26 @@ int sizes_of(const ffai_encoder_attn_desc* d, Sizes* z) {
   return FFAI_OK;
 }
 
+// The layout every pass of a call runs in: the first (fullest) pass's activation regions, which
+// no shorter pass exceeds, and an attention region as large as the largest need of any pass. A
+// shorter last pass can need more attention workspace than a full one: its grid is smaller, so
+// the planner splits its keys into more pieces (whisper-large-v3 width, 6 windows of 300 frames:
+// the 5-window pass needs no partials, the 1-window remainder ~6 MB).
+int call_sizes(const ffai_encoder_attn_desc* d, Sizes* z) {
+  const int wpp = windows_per_pass(d);
+  const ffai_encoder_attn_desc first = pass_desc(d, wpp);
+  int rc = sizes_of(&first, z);
+  if (rc != FFAI_OK) return rc;
+  if (const int rem = d->batch % wpp) {
+    const ffai_encoder_attn_desc last = pass_desc(d, rem);
+    Sizes zl;
+    if ((rc = sizes_of(&last, &zl)) != FFAI_OK) return rc;
+    z->total += std::max(z->attn, zl.attn) - z->attn;
+    z->attn = std::max(z->attn, zl.attn);
+  }
+  return FFAI_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -235,10 +255,8 @@ int ffai_encoder_attn_workspace_bytes(const ffai_encoder_attn_desc* d, size_t* b
   if (!bytes) return api_fail(FFAI_ERR_INVALID, "null bytes pointer");
   int rc = check(d);
   if (rc != FFAI_OK) return rc;
-  // every pass fits the first (largest) one's layout
-  const ffai_encoder_attn_desc p = pass_desc(d, windows_per_pass(d));
   Sizes z;
-  rc = sizes_of(&p, &z);
+  rc = call_sizes(d, &z);
   if (rc != FFAI_OK) return rc;
   *bytes = z.total;
   return FFAI_OK;
@@ -325,9 +343,8 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   if (!packed && (!w->wq || !w->bq || !w->wk_scaled || !w->wv || !w->bv))
     return api_fail(FFAI_ERR_INVALID, "null pointer (give wq, bq, wk_scaled, wv, bv or wqkv, bqkv)");
   const int wpp = windows_per_pass(d);
-  const ffai_encoder_attn_desc first = pass_desc(d, wpp);
   Sizes z;
-  if ((rc = sizes_of(&first, &z)) != FFAI_OK) return rc;
+  if ((rc = call_sizes(d, &z)) != FFAI_OK) return rc;
   if (!workspace || workspace_bytes < z.total)
     return api_fail(FFAI_ERR_WORKSPACE, "workspace smaller than ffai_encoder_attn_workspace_bytes");
   if ((uintptr_t)workspace % 256) return api_fail(FFAI_ERR_INVALID, "workspace must be 256-byte aligned");
@@ -335,18 +352,13 @@ int ffai_encoder_attn_fwd(const ffai_encoder_attn_desc* d, const void* x,
   hipblasLtHandle_t h;
   if ((rc = handle_for_current(&h)) != FFAI_OK) return rc;
   // passes in window order, stream-ordered through the one workspace (the reference's loop over
-  // batch items); a last, shorter pass lays its buffers out within the first pass's regions
+  // batch items); every pass uses the call's layout z, whose attention region holds the largest
+  // need of any pass, so no pass is refused after an earlier one has written part of `out`
   const size_t window_bytes = (size_t)d->seq * d->n_state * 2;
   for (int b0 = 0; b0 < d->batch; b0 += wpp) {
     const ffai_encoder_attn_desc p = pass_desc(d, std::min(wpp, d->batch - b0));
-    Sizes zp;
-    if ((rc = sizes_of(&p, &zp)) != FFAI_OK) return rc;
-    // the pass's regions keep the first pass's offsets (each region of a shorter pass is no
-    // larger than the first pass's)
-    zp.q = z.q; zp.kt = z.kt; zp.v = z.v; zp.merged = z.merged; zp.gemm = z.gemm;
-    zp.attn = z.attn;
     rc = run_pass(&p, static_cast<const char*>(x) + b0 * window_bytes, w, packed,
-                  static_cast<char*>(out) + b0 * window_bytes, workspace, zp, h, stream);
+                  static_cast<char*>(out) + b0 * window_bytes, workspace, z, h, stream);
     if (rc != FFAI_OK) return rc;
   }
   return FFAI_OK;

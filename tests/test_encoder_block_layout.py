@@ -152,3 +152,25 @@ def test_one_pass_above_1500_rows_is_refused():
     got = ctypes.c_size_t(0)
     assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(got)) == \
         L.FFAI_ERR_INVALID
+
+
+@pytest.mark.parametrize("b,s,n,h", [(6, 300, 1280, 20), (4, 500, 768, 12), (3, 700, 1024, 16)])
+def test_a_shorter_last_pass_fits_the_attention_region(b, s, n, h):
+    """A call whose last pass holds fewer windows: that pass's smaller grid splits its keys into
+    more pieces and can need more attention workspace than a full pass. The call's attention
+    region must hold the largest need of any pass (large-v3, small and medium widths)."""
+    lib = L.load()
+    wpp = max(1, min(b, 1500 // s))
+    rem = b % wpp
+    assert rem, "each shape ends with a shorter pass"
+    need_full = max(attn_ws_bytes(lib, wpp, s, n, h, p) for p in (False, True))
+    need_rem = max(attn_ws_bytes(lib, rem, s, n, h, p) for p in (False, True))
+    assert need_rem > need_full  # the case a region sized by the first pass alone misses
+    d = L.EncoderAttnDesc()
+    d.dtype, d.batch, d.seq, d.n_state, d.n_head = L.BF16, b, s, n, h
+    got = ctypes.c_size_t(0)
+    assert lib.ffai_encoder_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(got)) == L.FFAI_OK
+    full = layout(lib, wpp, s, n, h)
+    others = full["total"][1] - (full["attn"][1] - full["attn"][0])  # q, kt, v, merged, gemm
+    attn_region = got.value - others
+    assert attn_region == align256(max(need_full, need_rem, COUNTER_BYTES))

@@ -105,3 +105,17 @@ def test_encoder_block_full_windows_equal_single_calls(gpu):
     for i in range(3):
         one = ea(dev(x[i:i + 1]))
         assert torch.equal(allx[i:i + 1], one), i
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_encoder_block_short_last_pass_at_large_v3_width(gpu, packed):
+    """Six 300-frame windows at whisper-large-v3 width (20 heads x 64) run as a five-window pass
+    and a one-window pass. The shorter pass's smaller grid splits its keys (about 6 MB of
+    partials, where the full pass needs none): the call's workspace holds it, and every window
+    matches the oracle."""
+    rng = np.random.default_rng(65)
+    x, ws = _case(rng, 6, 300, 1280, "bf16")
+    got, want = _run(gpu, x, ws, 20, "bf16", packed)
+    err = max_abs(got, want)
+    print(f"encoder block 6 x 300 large-v3 width packed={packed}: {err:.3e}")
+    assert err < TOL_BF16
