@@ -109,6 +109,8 @@ def load():
     L.ffai_attn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, sz, vp]
     L.ffai_attn_plan_info.argtypes = [dp, ctypes.POINTER(ctypes.c_int32)]
     L.ffai_attn_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp]
+    L.ffai_attn_noalloc_plan_info.argtypes = [dp, ctypes.POINTER(ctypes.c_int32),
+                                              ctypes.POINTER(sz)]
     L.ffai_attn_noalloc_scratch_bytes.restype = sz
     L.ffai_serves.argtypes = [tp, tp]
     L.ffai_attend.argtypes = [tp, tp, tp, ctypes.c_int, tp, vp, sz, vp]
@@ -148,6 +150,7 @@ def load():
     for name in ("ffai_probe_empty", "ffai_probe_read", "ffai_probe_pipes", "ffai_attn_serves",
                  "ffai_attn_workspace_bytes", "ffai_attn_fwd",
                  "ffai_attn_plan_info", "ffai_attn_plan_splits", "ffai_attn_fwd_noalloc",
+                 "ffai_attn_noalloc_plan_info",
                  "ffai_serves",
                  "ffai_attend", "ffai_attend_workspace_bytes", "ffai_attend_merged",
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
@@ -172,6 +175,15 @@ def plan_info(desc: AttnDesc) -> dict:
     check(load().ffai_attn_plan_splits(ctypes.byref(desc), sp))
     out.update(items=sp[0], split_items=(sp[1], sp[2]))
     return out
+
+
+def noalloc_plan_info(desc: AttnDesc) -> dict:
+    """The launch plan ffai_attn_fwd_noalloc uses for `desc` (vector-aligned operands) and the
+    scratch bytes it takes."""
+    info = (ctypes.c_int32 * 5)()
+    nbytes = ctypes.c_size_t(0)
+    check(load().ffai_attn_noalloc_plan_info(ctypes.byref(desc), info, ctypes.byref(nbytes)))
+    return {"info": tuple(info), "bytes": nbytes.value}
 
 
 def set_fwd_split_override(items: int, pieces: int) -> None:

@@ -172,7 +172,9 @@ struct Plan {
 // partials the unit's last workgroup merges in the same launch (counters at the workspace's
 // start). When the units alone leave the GPU short of workgroups, a workgroup takes fewer tiles
 // so that more of them stream keys at once.
-bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
+// `max_ws`: the workspace available; a split that would need more is coarsened (more tiles per
+// workgroup) until it fits, down to no split.
+bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, Plan* p) {
   const int group = d->heads_q / d->heads_kv;
   const int64_t rows = (int64_t)group * d->q_len;
   if (d->q_dtype == FFAI_F32 || rows > 32 || !allow_split) return false;
@@ -201,6 +203,12 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
   if (units > ffai::kCounterSlots) tps = n_tiles;
   if ((n_tiles + tps - 1) / tps > ffai::kMaxDecodeSplits)
     tps = (n_tiles + ffai::kMaxDecodeSplits - 1) / ffai::kMaxDecodeSplits;
+  // every split is there for speed only: under a workspace cap, fewer and longer splits
+  auto split_bytes = [&](int64_t t) {
+    const int64_t n = (n_tiles + t - 1) / t;
+    return n > 1 ? ffai::kCounterBytes + (size_t)(units * n * rows * (d->head_dim + 2) * 4) : 0;
+  };
+  while (tps < n_tiles && split_bytes(tps) > max_ws) ++tps;
   p->decode = true;
   // as many waves as tiles per workgroup (1, 2, 4 or max_waves); a workgroup's waves loop when
   // it holds more tiles than that
@@ -212,20 +220,18 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, Plan* p) {
   p->tiles_per_split = (int)tps;
   p->n_split = (int)((n_tiles + tps - 1) / tps);
   p->n_work = (int)(units * p->n_split);
-  p->ws_bytes = p->n_split > 1
-                    ? ffai::kCounterBytes + (size_t)units * p->n_split * rows * (d->head_dim + 2) * 4
-                    : 0;
+  p->ws_bytes = split_bytes(tps);
   return true;
 }
 
 // `vector_ok`: the operands admit the decode kernel's vector accesses (it has no element-wise
 // path; misaligned decode shapes take fwd_kernel).
-// `max_ws`: the workspace available; splits the planner makes only for balance are dropped
-// rather than exceed it.
+// `max_ws`: the workspace available. Every split serves speed only, so a plan whose partials
+// would exceed it runs its split items in fewer pieces, or whole, instead.
 Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
                size_t max_ws = SIZE_MAX) {
   Plan p{};
-  if (vector_ok && plan_decode(d, allow_split, &p)) return p;
+  if (vector_ok && plan_decode(d, allow_split, max_ws, &p)) return p;
   const int64_t bh = (int64_t)d->batch * d->heads_q;
   const bool f32 = d->q_dtype == FFAI_F32;
   const int n_tiles = (d->kv_len + ffai::kBlockN - 1) / ffai::kBlockN;
@@ -288,7 +294,6 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   }();
   if (forced_splits > 0) want = forced_splits;
   int64_t lo = 0, hi = want > 1 ? items : 0;
-  bool optional = false;  // a split for balance only
   if (want == 1 && !f32) {
     // Long grids split only the items that would leave the GPU partly idle at the end.
     // Resident workgroups: four-wave x 64 rows and head_dim 128 two per CU (VGPRs, LDS), four
@@ -311,7 +316,7 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
       if (longest >= 4 && longest * 5 > 6 * (total / slots)) {
         int64_t n = 0;  // rank order: query blocks descending, all (batch, head) of each
         for (int64_t qb = p.n_qblk - 1; qb >= 0 && 2 * tiles_of(qb) > longest; --qb) n += nbh;
-        if (n > 0) { want = 2; lo = 0; hi = n; optional = true; }
+        if (n > 0) { want = 2; lo = 0; hi = n; }
       }
     } else if (items > slots && n_tiles >= 8) {
       // Non-causal: a last round of at most a quarter of the slots runs its items in 4 pieces.
@@ -319,7 +324,7 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
       // in 4 pieces against 88.0 unsplit (2: 78.1, 6: 87.5).
       const int64_t tail = items % slots;
       if (tail > 0 && 4 * tail <= slots) {
-        want = 4; lo = items - tail; hi = items; optional = true;
+        want = 4; lo = items - tail; hi = items;
       } else if (tail > 0 && 3 * tail >= slots && p.variant == ffai::kWave4x2) {
         // A last round of at least a third of the slots: the last k items go in n pieces so
         // that the last round holds exactly one work per slot, tail - k whole items and k * n
@@ -329,7 +334,7 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
         // 64 in 3 pieces, also 2048 works, 213.2; 2048 +- 64 or 128 works 215-221).
         const int64_t n = 2 * tail >= slots ? 2 : 3;
         const int64_t k = (slots - tail) / (n - 1);
-        if (k >= 1 && k <= tail) { want = n; lo = items - k; hi = items; optional = true; }
+        if (k >= 1 && k <= tail) { want = n; lo = items - k; hi = items; }
       }
     }
   }
@@ -349,10 +354,12 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // no piece without tiles: as many pieces as ceil(tiles / n)-tile ranges cover the keys (a
   // forced layout is kept as given)
   if (want > 1 && !overridden) want = (n_tiles + (n_tiles + want - 1) / want - 1) / ((n_tiles + want - 1) / want);
-  const int64_t want_bytes = (hi - lo) * want * bm * (d->head_dim + 2) * 4;
+  auto bytes_of = [&](int64_t n) { return (hi - lo) * n * bm * (d->head_dim + 2) * 4; };
+  // under a workspace cap, fewer pieces (a forced layout is kept as given: it is refused later
+  // if it does not fit)
+  while (!overridden && want > 1 && ffai::kCounterBytes + (size_t)bytes_of(want) > max_ws) --want;
   if (allow_split && want > 1 && hi > lo && hi - lo <= ffai::kCounterSlots &&
-      want_bytes < (int64_t(1) << 31) &&
-      !(optional && ffai::kCounterBytes + (size_t)want_bytes > max_ws)) {
+      bytes_of(want) < (int64_t(1) << 31)) {
     p.n_split = (int)want;
     p.tiles_per_split = (n_tiles + p.n_split - 1) / p.n_split;
     p.split_lo = (int)lo;
@@ -379,9 +386,9 @@ size_t plan_ws_bytes(const ffai_attn_desc* d) {
 // ---- allocation-free entry point: a library-owned split-key scratch per device ----------------
 // ffai_attn_fwd_noalloc keeps the split counters and split-key partials in this array instead
 // of a caller workspace (the counters start at zero, as a static array does, and every call
-// leaves them zero). Every plan of ffai_attn_fwd needs at most ~51 MB of workspace (head_dim
-// 128, 16-bit, three splits of a grid under 256 workgroups); a plan above kScratchBytes is
-// refused.
+// leaves them zero). Its plans are ffai_attn_fwd's with the workspace capped at kScratchBytes:
+// a plan whose partials would not fit runs its split items in fewer pieces, or whole (splits
+// serve speed only), so only a layout forced by ffai_set_fwd_split_override can be refused.
 // In host code `scratch` names a host-side stand-in, not device memory: the device address is
 // taken once per device with hipGetSymbolAddress (that device current) and kept in
 // g_scratch_ptr; only that address is handed to kernels. The array lives until the process
@@ -653,6 +660,23 @@ int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]) {
   info[2] = p.n_split;
   info[3] = p.tiles_per_split;
   info[4] = p.n_work;
+  return FFAI_OK;
+}
+
+int ffai_attn_noalloc_plan_info(const ffai_attn_desc* d, int32_t info[5], size_t* bytes) {
+  if (!info || !bytes) return fail(FFAI_ERR_INVALID, "null info or bytes pointer");
+  *bytes = 0;
+  std::string why;
+  const int rc = check_desc(d, &why);
+  if (rc == FFAI_DECLINED) return fail(FFAI_DECLINED, "declined: " + why);
+  if (rc != FFAI_OK) return fail(rc, why);
+  const Plan p = make_plan(d, true, true, kScratchBytes);
+  info[0] = p.decode ? 1 : 0;
+  info[1] = p.decode ? p.waves : p.variant;
+  info[2] = p.n_split;
+  info[3] = p.tiles_per_split;
+  info[4] = p.n_work;
+  *bytes = p.ws_bytes;
   return FFAI_OK;
 }
 

@@ -108,9 +108,13 @@ int ffai_attn_fwd(const ffai_attn_desc* d, const void* q, const void* k, const v
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): ffai_attn_fwd
  * without a workspace argument. The split-key partials go to a scratch array the library owns,
  * one per device (ffai_attn_noalloc_scratch_bytes(): 48 MiB, held from the first call on a
- * device until the process ends); the call allocates nothing and otherwise runs exactly
- * ffai_attn_fwd's plan and kernels, so its output is the same. A shape whose partials exceed
- * the scratch returns FFAI_ERR_WORKSPACE. Every call on one device shares that device's
+ * device until the process ends); the call allocates nothing. It runs ffai_attn_fwd's kernels
+ * on ffai_attn_fwd's plan capped to the scratch: when that plan's partials fit (every shape of
+ * the whisper and prefill workloads), the plans are the same and so is the output, bit for bit;
+ * otherwise its split items run in fewer key pieces, or whole, and the output equals
+ * ffai_attn_fwd's to f32 rounding (ffai_attn_noalloc_plan_info reports the plan). Only a layout
+ * forced by ffai_set_fwd_split_override that exceeds the scratch returns FFAI_ERR_WORKSPACE.
+ * Every call on one device shares that device's
  * scratch: calls that may overlap on one device (different streams, unordered) race; calls
  * ordered on one stream, and replays of captured graphs, do not. The scratch keeps the last
  * call's partials; nothing in it needs clearing between calls. */
@@ -129,6 +133,11 @@ size_t ffai_attn_noalloc_scratch_bytes(void);
  * info[4]: workgroups. Returns FFAI_OK, FFAI_DECLINED or FFAI_ERR_INVALID as
  * ffai_attn_workspace_bytes. */
 int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]);
+
+/* Diagnostic, no counterpart in the reference: the plan ffai_attn_fwd_noalloc runs for `d`
+ * (info as ffai_attn_plan_info) and the scratch bytes it uses (*bytes, at most
+ * ffai_attn_noalloc_scratch_bytes()). Returns as ffai_attn_plan_info. */
+int ffai_attn_noalloc_plan_info(const ffai_attn_desc* d, int32_t info[5], size_t* bytes);
 
 /* Diagnostic, no counterpart in the reference: which work items of the fused kernel's plan for
  * `d` run as key-split pieces. Items are the (batch, head, query block) triples in dispatch rank

@@ -121,6 +121,8 @@ extern "C" {
     pub fn ffai_attn_noalloc_scratch_bytes() -> usize;
     pub fn ffai_attn_plan_info(d: *const ffai_attn_desc, info: *mut i32) -> c_int;
     pub fn ffai_attn_plan_splits(d: *const ffai_attn_desc, info: *mut i32) -> c_int;
+    pub fn ffai_attn_noalloc_plan_info(d: *const ffai_attn_desc, info: *mut i32,
+                                       bytes: *mut usize) -> c_int;
 
     // ---- include/ffai_attn.h: mirrors of flash_attn.rs
     pub fn ffai_serves(kt: *const ffai_tensor, v: *const ffai_tensor) -> c_int;

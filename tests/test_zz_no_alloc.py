@@ -1,9 +1,11 @@
 """The allocation-free entry point ffai_attn_fwd_noalloc against ffai_attn_fwd, through the C ABI.
 
 ffai_attn_fwd_noalloc runs ffai_attn_fwd's plan and kernels with the split-key partials in the
-library's per-device scratch instead of a caller workspace, so on the same inputs its output
-must equal ffai_attn_fwd's bit for bit. Each case makes two calls in a row, the second on a
-smaller input, so the second call runs over the partials the first one left in the scratch.
+library's per-device scratch instead of a caller workspace. Where ffai_attn_fwd's plan fits the
+scratch (every shape below) the plans are the same, so on the same inputs its output must equal
+ffai_attn_fwd's bit for bit; a larger plan runs with fewer key pieces (checked on the CPU). Each
+GPU case makes two calls in a row, the second on a smaller input, so the second call runs over
+the partials the first one left in the scratch.
 """
 
 from __future__ import annotations
@@ -157,3 +159,45 @@ def test_refuses_partials_above_the_scratch():
                                          None) == L.FFAI_DECLINED
     finally:
         L.set_fwd_split_override(*prev)
+
+
+@pytest.mark.parametrize("args", [
+    # f32, head_dim 64, 42 heads x 3000 rows: ffai_attn_fwd plans ~68 MB of partials
+    (L.F32, L.F32, L.F32, 1, 42, 42, 3000, 3000, 64, L.K_TRANSPOSED, 0),
+    # bf16 causal, 256 heads x 300 rows: a ~66 MB split for balance
+    (L.BF16, L.BF16, L.BF16, 1, 256, 256, 300, 300, 64, L.K_ROWS, 1),
+    # the workloads' shapes, whose plans fit
+    (L.F32, L.F32, L.F32, 1, 6, 6, 1500, 1500, 64, L.K_TRANSPOSED, 0),
+    (L.BF16, L.BF16, L.BF16, 8, 12, 12, 1500, 1500, 64, L.K_TRANSPOSED, 0),
+    (L.BF16, L.BF16, L.BF16, 16, 20, 20, 1500, 1500, 64, L.K_TRANSPOSED, 0),
+    (L.BF16, L.BF16, L.BF16, 1, 12, 2, 4096, 4096, 128, L.K_ROWS, 1),
+    (L.BF16, L.BF16, L.F32, 5, 16, 16, 1, 1500, 64, L.K_ROWS, 0),
+    (L.F32, L.F16, L.F32, 1, 16, 16, 1, 1500, 64, L.K_TRANSPOSED, 0),
+    # large decode grids: many units, long caches
+    (L.BF16, L.BF16, L.F32, 256, 32, 8, 4, 32768, 128, L.K_ROWS, 0),
+    (L.F16, L.F16, L.F16, 1024, 16, 16, 1, 8192, 64, L.K_ROWS, 0),
+    (L.F32, L.F32, L.F32, 64, 40, 40, 700, 700, 64, L.K_ROWS, 0),
+])
+def test_noalloc_plan_is_the_fwd_plan_capped_to_the_scratch(args):
+    """ffai_attn_fwd_noalloc's plan equals ffai_attn_fwd's whenever that plan's partials fit the
+    scratch; otherwise it keeps the kernel and launch shape and takes fewer key pieces, within
+    the scratch. No default plan is refused."""
+    lib = L.load()
+    cap = lib.ffai_attn_noalloc_scratch_bytes()
+    *dims, layout, causal = args
+    d = L.AttnDesc()
+    lib.ffai_attn_desc_init(ctypes.byref(d), *dims, layout)
+    d.causal = causal
+    n = ctypes.c_size_t(0)
+    assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == L.FFAI_OK
+    fwd = L.plan_info(d)
+    fwd_info = (1 if fwd["kernel"] == "decode" else 0,
+                fwd["shape"] if fwd["kernel"] == "decode" else
+                ("wave1", "wave4", "wave4x2").index(fwd["shape"]),
+                fwd["splits"], fwd["tiles_per_split"], fwd["workgroups"])
+    na = L.noalloc_plan_info(d)
+    assert na["bytes"] <= cap
+    if n.value <= cap:
+        assert na["info"] == fwd_info
+    else:
+        assert na["info"][:2] == fwd_info[:2] and na["info"][2] < fwd_info[2]
