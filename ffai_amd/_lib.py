@@ -124,6 +124,8 @@ def load():
     L.ffai_set_decode_tiles_per_wg.argtypes = [ctypes.c_int]
     L.ffai_set_decode_tiles_per_wg.restype = None
     L.ffai_attn_plan_splits.argtypes = [dp, ctypes.POINTER(ctypes.c_int32)]
+    L.ffai_set_geometry_override.argtypes = [ctypes.c_int, ctypes.c_int]
+    L.ffai_set_geometry_override.restype = None
     L.ffai_set_fwd_split_override.argtypes = [ctypes.c_int, ctypes.c_int]
     L.ffai_set_fwd_split_override.restype = None
     L.ffai_get_fwd_split_override.argtypes = [ctypes.POINTER(ctypes.c_int)] * 2
@@ -184,6 +186,11 @@ def noalloc_plan_info(desc: AttnDesc) -> dict:
     nbytes = ctypes.c_size_t(0)
     check(load().ffai_attn_noalloc_plan_info(ctypes.byref(desc), info, ctypes.byref(nbytes)))
     return {"info": tuple(info), "bytes": nbytes.value}
+
+
+def set_geometry_override(cus: int, xcds: int) -> None:
+    """Plan for a device of `cus` CUs in `xcds` XCDs (0, 0: the current device's geometry)."""
+    load().ffai_set_geometry_override(int(cus), int(xcds))
 
 
 def set_fwd_split_override(items: int, pieces: int) -> None:

@@ -46,6 +46,53 @@ int check_device() {
   return FFAI_OK;
 }
 
+// ---- device geometry: CUs and XCDs of the current device, which the launch plans balance over.
+// An MI355X in its default (single-partition) mode has 256 CUs in 8 XCDs; a partitioned one
+// shows each partition as a device with its share. Without a device (planning on a host with no
+// GPU) the plans assume the full chip. ffai_set_geometry_override replaces it (tests, sweeps).
+struct Geometry {
+  int cus = 256;
+  int xcds = 8;
+};
+std::atomic<int> g_geo_cus[kMaxDevices], g_geo_xcds[kMaxDevices];  // 0: not yet read
+std::atomic<int> g_geo_override_cus{0}, g_geo_override_xcds{0};
+
+Geometry device_geometry() {
+  Geometry g;
+  const int oc = g_geo_override_cus.load(std::memory_order_relaxed);
+  const int ox = g_geo_override_xcds.load(std::memory_order_relaxed);
+  if (oc > 0 && ox > 0) {
+    g.cus = oc;
+    g.xcds = ox;
+    return g;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return g;
+  int cus = g_geo_cus[dev].load(std::memory_order_acquire);
+  int xcds = g_geo_xcds[dev].load(std::memory_order_acquire);
+  if (cus == 0 || xcds == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1)
+      cus = g.cus;
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess ||
+        xcds < 1)
+      xcds = g.xcds;
+    g_geo_xcds[dev].store(xcds, std::memory_order_release);
+    g_geo_cus[dev].store(cus, std::memory_order_release);
+  }
+  g.cus = cus;
+  g.xcds = xcds;
+  return g;
+}
+
+// log2 of the XCD count when it is a power of two (the remap deals workgroups by mask and
+// shift), else -1 (no remap).
+int xcd_shift_of(int xcds) {
+  int s = 0;
+  while ((1 << s) < xcds) ++s;
+  return (1 << s) == xcds ? s : -1;
+}
+
 // ---- knobs (mirror of knobs::DECODE_MIN_KEYS, knobs.rs:163-168) ------------------------------
 std::atomic<int> g_decode_min_keys{-1};
 
@@ -163,6 +210,8 @@ struct Plan {
   // fwd: items [split_lo, split_hi) of n_items run as n_split pieces; dispatch sections
   int n_items, split_lo, split_hi, sec1_work;
   bool xcd_remap;
+  int xcd_shift;  // log2 of the XCDs the sections are rounded to (0: one)
+  int cus;
   size_t ws_bytes;
 };
 
@@ -174,7 +223,8 @@ struct Plan {
 // so that more of them stream keys at once.
 // `max_ws`: the workspace available; a split that would need more is coarsened (more tiles per
 // workgroup) until it fits, down to no split.
-bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, Plan* p) {
+bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, const Geometry& geo,
+                 Plan* p) {
   const int group = d->heads_q / d->heads_kv;
   const int64_t rows = (int64_t)group * d->q_len;
   if (d->q_dtype == FFAI_F32 || rows > 32 || !allow_split) return false;
@@ -190,8 +240,8 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, Plan*
   // second launch cost. Measured, beam-5 whisper-medium step (24 layers, graphs), tiles per
   // workgroup for the cross-attention (16 heads x 24 tiles): 1: 397 us, 2: 249, 3: 224, 4: 225,
   // 6: 241, 8: 253, 24 (unsplit): 375; the self-attention's 80 units split at all: 191-212
-  // against 165 unsplit.
-  constexpr int64_t kMinWorkgroups = 64, kSplitWorkgroups = 128;
+  // against 165 unsplit. (Measured on 256 CUs: the bounds scale with the device's CUs.)
+  const int64_t kMinWorkgroups = std::max(1, geo.cus / 4), kSplitWorkgroups = std::max(1, geo.cus / 2);
   int64_t tps = max_waves;
   if (units * ((n_tiles + tps - 1) / tps) < kMinWorkgroups)
     tps = std::max<int64_t>(1, n_tiles * units / kSplitWorkgroups);
@@ -231,7 +281,11 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, Plan*
 Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
                size_t max_ws = SIZE_MAX) {
   Plan p{};
-  if (vector_ok && plan_decode(d, allow_split, max_ws, &p)) return p;
+  const Geometry geo = device_geometry();
+  const int64_t cus = geo.cus;
+  p.cus = geo.cus;
+  p.xcd_shift = std::max(0, xcd_shift_of(geo.xcds));
+  if (vector_ok && plan_decode(d, allow_split, max_ws, geo, &p)) return p;
   const int64_t bh = (int64_t)d->batch * d->heads_q;
   const bool f32 = d->q_dtype == FFAI_F32;
   const int n_tiles = (d->kv_len + ffai::kBlockN - 1) / ffai::kBlockN;
@@ -242,13 +296,13 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   p.variant = ffai::kWave1;
   if (d->q_len > 32) p.variant = ffai::kWave4;
   if (!f32 && d->head_dim == 64 && d->q_len >= 256) p.variant = ffai::kWave4x2;
-  if (p.variant == ffai::kWave4x2 && work_of(p.variant) < 256) p.variant = ffai::kWave4;
+  if (p.variant == ffai::kWave4x2 && work_of(p.variant) < cus) p.variant = ffai::kWave4;
   // A one-wave workgroup holds a whole tile ring (48 KB of LDS in 16-bit, 68 KB in f32) for
   // one wave, so at most three (two) of them run per CU. Short grids of 16-bit rows fewer than
   // the encoder's (a prompt step: 228 rows) still run best on it; long runs and f32 keep four
   // waves and split the keys instead (measured: whisper-large-v3 window, 20 heads x 1500 rows,
   // bf16: 42.5 against 69.7 us; whisper-tiny f32: 66 against 154 us).
-  if (p.variant == ffai::kWave4 && work_of(p.variant) < 256 && !f32 && d->q_len < 256)
+  if (p.variant == ffai::kWave4 && work_of(p.variant) < cus && !f32 && d->q_len < 256)
     p.variant = ffai::kWave1;
   // FFAI_ATTN_VARIANT (0, 1, 2) forces a launch shape where it is instantiated: a tuning knob.
   static const int forced = [] {
@@ -278,14 +332,15 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // 15.7 in 4 and 19.2 in 7 (896 workgroups: a second round). One-wave f32 grids (two per CU)
   // keep about 512 workgroups: f32 decode over 1500 keys, 6 heads: 25.9 us in 24 pieces, 32.7
   // in 8, 193 whole; 80 items: 55.8 in 7, 73.9 in 4, 86.8 in 24.
+  // (Measured on 256 CUs; the slot counts below scale with the device's CUs.)
   int64_t want = 1;
   if (p.variant == ffai::kWave1) {
-    if (f32 && items < 512) want = std::min<int64_t>(24, (512 + items - 1) / items);
-    else if (!f32 && items < 768) want = std::min<int64_t>(ffai::kMaxFwdSplits, 768 / items);
-  } else if (items < 256) {
-    want = f32 ? 512 / items : std::max<int64_t>(1, std::min<int64_t>(3, 256 / items));
-  } else if (f32 && items < 1024) {
-    want = (4096 + 4 * items - 1) / (4 * items);
+    if (f32 && items < 2 * cus) want = std::min<int64_t>(24, (2 * cus + items - 1) / items);
+    else if (!f32 && items < 3 * cus) want = std::min<int64_t>(ffai::kMaxFwdSplits, 3 * cus / items);
+  } else if (items < cus) {
+    want = f32 ? 2 * cus / items : std::max<int64_t>(1, std::min<int64_t>(3, cus / items));
+  } else if (f32 && items < 4 * cus) {
+    want = (16 * cus + 4 * items - 1) / (4 * items);
   }
   // FFAI_ATTN_SPLITS (> 0) forces the pieces of every item: a tuning knob.
   static const int forced_splits = [] {
@@ -298,7 +353,7 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
     // Long grids split only the items that would leave the GPU partly idle at the end.
     // Resident workgroups: four-wave x 64 rows and head_dim 128 two per CU (VGPRs, LDS), four
     // waves x 32 rows at head_dim 64 and one-wave shapes three.
-    const int64_t slots = 256 * ((p.variant == ffai::kWave4x2 || d->head_dim == 128) ? 2 : 3);
+    const int64_t slots = cus * ((p.variant == ffai::kWave4x2 || d->head_dim == 128) ? 2 : 3);
     if (d->causal) {
       // Causal, rank order longest first: when the longest item is well above a resident slot's
       // share of the work, it bounds the launch; the items longer than half the longest go in 2
@@ -371,7 +426,7 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // go to the XCDs in contiguous runs (one head's query blocks, one item's pieces share an L2);
   // split items at the end of the grid form the second section, so that they are dealt to every
   // XCD and dispatched after the whole items.
-  p.xcd_remap = !d->causal;
+  p.xcd_remap = !d->causal && xcd_shift_of(geo.xcds) > 0;
   p.sec1_work = (p.split_hi > p.split_lo && p.split_lo > 0) ? p.split_lo : p.n_work;
   const size_t part_bytes = (size_t)pieces * bm * (d->head_dim + 2) * 4;
   p.ws_bytes = pieces > 0 ? ffai::kCounterBytes + part_bytes : 0;
@@ -499,7 +554,12 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
   p.split_lo = pl.split_lo; p.split_hi = pl.split_hi; p.n_split = pl.n_split;
   p.n_work = pl.n_work;
   p.sec1_work = pl.sec1_work;
-  p.sec1_wgs = (pl.sec1_work + 7) / 8 * 8;
+  p.xcd_shift = pl.xcd_shift;
+  p.cus = pl.cus;
+  {
+    const int xr = 1 << pl.xcd_shift;
+    p.sec1_wgs = (pl.sec1_work + xr - 1) / xr * xr;
+  }
   p.xcd_remap = pl.xcd_remap ? 1 : 0;
   p.counters = static_cast<int32_t*>(ws);
   p.aligned = aligned;
@@ -772,6 +832,12 @@ int ffai_get_decode_tiles_per_wg(void) { return decode_tiles_per_wg(); }
 
 void ffai_set_decode_tiles_per_wg(int n) {
   if (n >= 0) g_decode_tps.store(n, std::memory_order_relaxed);
+}
+
+void ffai_set_geometry_override(int cus, int xcds) {
+  const bool on = cus > 0 && xcds > 0;
+  g_geo_override_xcds.store(on ? xcds : 0, std::memory_order_relaxed);
+  g_geo_override_cus.store(on ? cus : 0, std::memory_order_relaxed);
 }
 
 void ffai_set_fwd_split_override(int items, int pieces) {

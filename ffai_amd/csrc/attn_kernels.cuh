@@ -26,7 +26,7 @@
 //     exact max, with the accumulator rescaled; that is rare for real scores, and it keeps every
 //     weight and sum finite in f32.
 //   * Workgroup ids are remapped so that all query blocks of one (batch, kv-head) run on the
-//     same XCD (the hardware deals workgroup i to XCD i % 8) and share that XCD's L2.
+//     same XCD (the hardware deals workgroup i to XCD i % XCDs) and share that XCD's L2.
 //   * Items (batch, head, query block) may run as several pieces, each a contiguous key range:
 //     every item of a short grid, the last round's items of a long one, the longest items of a
 //     causal one. Pieces write partial (O, m, l) to the workspace and the item's last piece to
@@ -83,12 +83,13 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   // ---- which work (an item, or one piece of a split item) this workgroup computes
   const int hw = blockIdx.x;
   int work;
+  const int xs = p.xcd_shift, xm = (1 << xs) - 1;  // XCDs: 1 << xs
   if (hw < p.sec1_wgs) {
-    work = p.xcd_remap ? (hw & 7) * (p.sec1_wgs >> 3) + (hw >> 3) : hw;
+    work = p.xcd_remap ? (hw & xm) * (p.sec1_wgs >> xs) + (hw >> xs) : hw;
     if (work >= p.sec1_work) return;
   } else {
-    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;  // n: a multiple of 8
-    work = p.sec1_work + (p.xcd_remap ? (x & 7) * (n >> 3) + (x >> 3) : x);
+    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;  // n: a multiple of 1 << xs
+    work = p.sec1_work + (p.xcd_remap ? (x & xm) * (n >> xs) + (x >> xs) : x);
     if (work >= p.n_work) return;
   }
   const int n_pieces = (p.split_hi - p.split_lo) * p.n_split;

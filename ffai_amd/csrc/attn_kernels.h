@@ -34,12 +34,15 @@ struct FwdParams {
   int32_t split_lo, split_hi;
   int32_t n_split;           // pieces per split item (1 when no item is split)
   int32_t n_work;            // items + (split_hi - split_lo) * (n_split - 1): works in rank order
-  // Dispatch: works [0, sec1_work) take the first sec1_wgs workgroups (a multiple of 8), the
-  // rest the remaining ones. With xcd_remap each section deals its works to the 8 XCDs in
-  // contiguous runs (hardware workgroup i goes to XCD i % 8), so neighbouring works (one head's
-  // query blocks, one item's pieces) share an L2; without it works go in rank order.
+  // Dispatch: works [0, sec1_work) take the first sec1_wgs workgroups (a multiple of the XCD
+  // count X = 1 << xcd_shift), the rest the remaining ones. With xcd_remap each section deals
+  // its works to the X XCDs in contiguous runs (hardware workgroup i goes to XCD i % X), so
+  // neighbouring works (one head's query blocks, one item's pieces) share an L2; without it
+  // works go in rank order.
   int32_t sec1_work, sec1_wgs;
   int32_t xcd_remap;
+  int32_t xcd_shift;         // log2 of the device's XCD count (sections are whole XCD rounds)
+  int32_t cus;               // the device's CUs (host side: launch shaping)
   int32_t aligned;           // every operand admits the kernels' vector loads and stores
   int32_t dma;               // 16-bit: whole tiles may go global -> LDS by DMA (aligned, and
                              // each lane's byte offset within a K or V tile fits 32 bits)

@@ -9,12 +9,13 @@ namespace {
 template <int MODE, int KVT, int OUTT, int D, bool KT, int NW, int QW>
 hipError_t launch_one(const FwdParams& p, hipStream_t s) {
   // two dispatch sections, each in whole XCD rounds
-  const unsigned grid = (unsigned)(p.sec1_wgs + (p.n_work - p.sec1_work + 7) / 8 * 8);
+  const int xr = 1 << p.xcd_shift;
+  const unsigned grid = (unsigned)(p.sec1_wgs + (p.n_work - p.sec1_work + xr - 1) / xr * xr);
   // Head_dim 128, four waves: 80 KB of LDS and <= 256 VGPRs admit two workgroups per CU. A grid
   // of fewer than two per CU then piles pairs onto some CUs and leaves others idle; 16 KB of
   // unused dynamic LDS keeps such a grid at one per CU (Qwen2-VL prefill, 384 workgroups:
   // 446 TFLOP/s against 407 with pairs; with 1536 workgroups pairs win, 770 against 585).
-  const size_t pad = (MODE != kF32 && D == 128 && NW == 4 && p.n_work < 512) ? 16384 : 0;
+  const size_t pad = (MODE != kF32 && D == 128 && NW == 4 && p.n_work < 2 * p.cus) ? 16384 : 0;
   hipLaunchKernelGGL((fwd_kernel<MODE, KVT, OUTT, D, KT, NW, QW>), dim3(grid), dim3(NW * 64), pad,
                      s, p);
   return hipGetLastError();

@@ -209,6 +209,13 @@ void ffai_set_decode_tiles_per_wg(int n);
 void ffai_set_fwd_split_override(int items, int pieces);
 void ffai_get_fwd_split_override(int* items, int* pieces);
 
+/* Tuning and test hook, no counterpart in the reference: the device geometry the launch plans
+ * balance over. By default the current device's CUs and XCDs (hipDeviceAttributeMultiprocessorCount,
+ * hipDeviceAttributeNumberOfXccs: 256 and 8 on an MI355X in single-partition mode, a share of them
+ * per partition otherwise; 256 and 8 when no device is visible). cus > 0 and xcds > 0 replace it
+ * for every device; 0, 0 restores it. It changes plans, never results beyond f32 rounding. */
+void ffai_set_geometry_override(int cus, int xcds);
+
 /* Human-readable description of the last error on the calling thread ("" if none). */
 const char* ffai_attn_last_error(void);
 
