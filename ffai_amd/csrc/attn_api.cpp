@@ -229,6 +229,12 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, const
   const int64_t rows = (int64_t)group * d->q_len;
   if (d->q_dtype == FFAI_F32 || rows > 32 || !allow_split) return false;
   if (d->k_layout == FFAI_K_TRANSPOSED && d->kv_len < 4) return false;  // 4-key chunk loads
+  // the DMA addresses a tile's rows (head_dim rows of K^T, 64 key rows of K and V) by 32-bit
+  // byte offsets from the tile's first row
+  const int64_t lim = int64_t(1) << 31;
+  if (int64_t(std::max(d->head_dim, ffai::kBlockN)) * d->k_strides[2] * 2 >= lim ||
+      int64_t(ffai::kBlockN) * d->v_strides[2] * 2 >= lim)
+    return false;
   const int64_t units = (int64_t)d->batch * d->heads_kv;
   int64_t kv_blk = d->kv_len;
   if (d->causal) kv_blk = std::min<int64_t>(kv_blk, (int64_t)d->q_offset + d->q_len);

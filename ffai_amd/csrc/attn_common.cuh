@@ -117,9 +117,12 @@ __device__ __forceinline__ u32x2 lds_tr(const uint16_t* p) {
 // bytes land at LDS byte address `lds_block` + 16 l. Issued as inline assembly so that the
 // compiler does not wait for it before unrelated LDS reads (it cannot tell which buffer a DMA
 // fills); the caller waits (vm_wait_all) before the barrier that publishes the data. M0 is set
-// here and used by nothing else in these kernels.
+// here and used by nothing else in these kernels. An LDS DMA that reads M0 right after a scalar
+// instruction wrote it needs one wait state on this GPU generation (the compiler inserts the
+// same s_nop before its own LDS DMA); inside inline assembly the compiler cannot, so the nop is
+// written here.
 __device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds_block) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :
                : "s"(lds_block), "v"(src)
                : "memory", "m0");
@@ -139,12 +142,12 @@ __device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t offse
   base = (const void*)(uintptr_t)sb;
   lds_block = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_block);
   if constexpr (NT)
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
                  :
                  : "s"(lds_block), "v"(offset), "s"(base)
                  : "memory", "m0");
   else
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
                  : "s"(lds_block), "v"(offset), "s"(base)
                  : "memory", "m0");

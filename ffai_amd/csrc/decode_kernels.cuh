@@ -134,10 +134,11 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   //      then patched element by element in LDS. Every address stays inside the operand.
   // The wave's own tile, whole and aligned: global -> LDS by DMA (16-byte chunks, lane L of
   // block j fills slot L of the block; the chunk placed there is the one the swizzle assigns).
-  // A 1 KB block holds 64 / (chunks per row) whole rows, so a lane's byte offset from its
-  // block's first row changes with the block only through the chunk permutation, and the
-  // wave-uniform base moves by whole rows: offsets in 32-bit lane arithmetic (equal ones merged
-  // by the compiler), bases in scalar registers.
+  // A 1 KB block holds 64 / (chunks per row) whole rows. Each lane's byte offset from the tile's
+  // first row (its row, the chunk permutation) is 32-bit lane arithmetic, the same for every
+  // tile (the host keeps a tile's rows within 2^31 bytes of its first); only the wave-uniform
+  // tile base moves, in scalar registers. (Block bases of their own, one 64-bit scalar pair per
+  // block and operand, made the compiler park them in vector-register lanes.)
   constexpr int KCH = KT ? BN / 8 : D / 8, KRB = 64 / KCH;  // K: chunks per row, rows per block
   constexpr int VCH = D / 8, VRB = 64 / VCH;
   const int kr = lane / KCH, kpc = lane % KCH, vr = lane / VCH, vpc = lane % VCH;
@@ -153,16 +154,14 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     for (int j = 0; j < KBUF / 512; ++j) {
       const int r = j * KRB + kr;
       const uint32_t off =
-          (uint32_t)(2 * (kr * p.k_st + 8 * (KT ? swz_kt(r, kpc) : swz_kr(r, kpc))));
-      if (KT || j * KRB < valid)
-        lds_dma16_sbase<true>(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
+          (uint32_t)(2 * (r * p.k_st + 8 * (KT ? swz_kt(r, kpc) : swz_kr(r, kpc))));
+      if (KT || j * KRB < valid) lds_dma16_sbase<true>(kbase, off, kla + j * 1024);
     }
 #pragma unroll
     for (int j = 0; j < VBUF / 512; ++j) {
       const int r = j * VRB + vr;
-      const uint32_t off = (uint32_t)(2 * (vr * p.v_st + 8 * swz_v(r, vpc)));
-      if (j * VRB < valid)
-        lds_dma16_sbase<true>(vbase + (int64_t)j * VRB * p.v_st * 2, off, vla + j * 1024);
+      const uint32_t off = (uint32_t)(2 * (r * p.v_st + 8 * swz_v(r, vpc)));
+      if (j * VRB < valid) lds_dma16_sbase<true>(vbase, off, vla + j * 1024);
     }
   };
   // The operand's last tile, when it has at least 8 keys but fewer than 64 (cross-attention over
@@ -182,8 +181,8 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
       if constexpr (KT) {
         const int c0 = kb + 8 * swz_kt(r, kpc);
         const int src = c0 + 8 <= p.Tk ? c0 : kb;
-        const uint32_t off = (uint32_t)(2 * (kr * p.k_st + (src - kb)));
-        lds_dma16_sbase<true>(kbase + (int64_t)j * KRB * p.k_st * 2, off, kla + j * 1024);
+        const uint32_t off = (uint32_t)(2 * (r * p.k_st + (src - kb)));
+        lds_dma16_sbase<true>(kbase, off, kla + j * 1024);
       } else {
         const int key = min(kb + r, klast);
         const uint32_t off = (uint32_t)(2 * ((key - kb) * p.k_st + 8 * swz_kr(r, kpc)));

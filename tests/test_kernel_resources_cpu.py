@@ -55,3 +55,19 @@ def test_encoder_kernels_keep_two_waves_per_simd(usage):
     assert enc and d128
     for k, v in {**enc, **d128}.items():
         assert v["occupancy"] >= 2 and v["vgprs"] + v["agprs"] <= 256, (k, v)
+
+
+def test_no_scalar_register_spills(usage):
+    """SGPR spills are parked in vector-register lanes (v_writelane / v_readlane), correct but a
+    change of the code the kernels were measured with: the fused kernel has none. The decode
+    kernel has none either, except its head_dim-128 K^T instantiations (no workload runs them:
+    head_dim-128 decode caches keep K as rows), which park at most a few predicates of the
+    register-staging tail path (checked in their ISA)."""
+    fwd = {k: v["sgpr_spill"] for k, v in _kernels(usage, "fwd_kernel").items()
+           if v.get("sgpr_spill")}
+    assert not fwd, fwd
+    dec = {k: v["sgpr_spill"] for k, v in _kernels(usage, "decode_kernel").items()
+           if v.get("sgpr_spill")}
+    d128_kt = {k: n for k, n in dec.items() if "ELi128ELb1E" in k}
+    assert dec.keys() == d128_kt.keys(), sorted(set(dec) - set(d128_kt))
+    assert all(n <= 8 for n in d128_kt.values()), d128_kt
