@@ -1,7 +1,7 @@
 """Build the gfx950 attention library in-tree: ffai_amd/libffai_attn.so.
 
 hipcc compiles the kernel instantiations (fwd_bf16.hip, fwd_f16.hip, fwd_f32.hip, decode.hip,
-decode_f16.hip),
+decode_f16.hip, decode_vec.hip),
 the decode-state kernels and their C ABI (kv_cache.hip), the decoder GEMVs (gemv.hip), the
 launch-floor probes (probe.hip), the launch dispatch (attn_launch.hip), the attention C ABI
 (attn_api.cpp) and the encoder attention block around hipBLASLt (encoder_attn.cpp) for gfx950
@@ -24,6 +24,7 @@ LIB_PATH = os.path.join(HERE, "libffai_attn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = [os.path.join(CSRC, n) for n in
            ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "decode_f16.hip",
+            "decode_vec.hip",
             "kv_cache.hip", "gemv.hip", "probe.hip", "attn_launch.hip", "attn_api.cpp",
             "encoder_attn.cpp")]
 LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]

@@ -223,23 +223,35 @@ struct Plan {
 // so that more of them stream keys at once.
 // `max_ws`: the workspace available; a split that would need more is coarsened (more tiles per
 // workgroup) until it fits, down to no split.
+// f32 queries take the f32 decode kernel (decode_vec_kernel: the reference's decode arms, one
+// query row per unit, head_dim 64); 16-bit ones the MFMA decode kernel (up to 32 rows).
 bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, const Geometry& geo,
                  Plan* p) {
   const int group = d->heads_q / d->heads_kv;
   const int64_t rows = (int64_t)group * d->q_len;
-  if (d->q_dtype == FFAI_F32 || rows > 32 || !allow_split) return false;
-  if (d->k_layout == FFAI_K_TRANSPOSED && d->kv_len < 4) return false;  // 4-key chunk loads
+  const bool vec = d->q_dtype == FFAI_F32;
+  if (!allow_split) return false;
+  if (vec ? (rows != 1 || d->head_dim != 64) : rows > 32) return false;
+  if (!vec && d->k_layout == FFAI_K_TRANSPOSED && d->kv_len < 4) return false;  // 4-key chunks
   // the DMA addresses a tile's rows (head_dim rows of K^T, 64 key rows of K and V) by 32-bit
   // byte offsets from the tile's first row
+  // (f32 decode kernel: a head's K^T columns and V rows, (head_dim x k_st) and (kv_len x v_st)
+  // elements, by 32-bit byte offsets from the head's base)
   const int64_t lim = int64_t(1) << 31;
-  if (int64_t(std::max(d->head_dim, ffai::kBlockN)) * d->k_strides[2] * 2 >= lim ||
-      int64_t(ffai::kBlockN) * d->v_strides[2] * 2 >= lim)
+  const int64_t es = vec ? (d->kv_dtype == FFAI_F32 ? 4 : 2) : 2;
+  if (int64_t(std::max(d->head_dim, ffai::kBlockN)) * d->k_strides[2] * es >= lim ||
+      int64_t(ffai::kBlockN) * d->v_strides[2] * es >= lim)
+    return false;
+  if (vec && ((int64_t)d->kv_len * d->v_strides[2] + d->head_dim) * es >= lim) return false;
+  if (vec && d->k_layout == FFAI_K_TRANSPOSED &&
+      ((int64_t)d->head_dim * d->k_strides[2] + d->kv_len) * es >= lim)
     return false;
   const int64_t units = (int64_t)d->batch * d->heads_kv;
   int64_t kv_blk = d->kv_len;
   if (d->causal) kv_blk = std::min<int64_t>(kv_blk, (int64_t)d->q_offset + d->q_len);
   const int64_t n_tiles = std::max<int64_t>(1, (kv_blk + ffai::kBlockN - 1) / ffai::kBlockN);
-  const int max_waves = d->head_dim == 64 ? 8 : 4;  // LDS: 16 KB (32 KB at head_dim 128) a wave
+  // 16-bit kernel: LDS, 16 KB (32 KB at head_dim 128) a wave; f32 kernel: registers
+  const int max_waves = (vec || d->head_dim == 64) ? 8 : 4;
   // A grid of at least kMinWorkgroups stays at max_waves tiles per workgroup; a smaller one is
   // split towards kSplitWorkgroups. A split costs the unit's last workgroup ~3.5 us of device-
   // scope round trips (its partial acknowledged, the counter, the other partials), about what a
@@ -249,7 +261,10 @@ bool plan_decode(const ffai_attn_desc* d, bool allow_split, size_t max_ws, const
   // against 165 unsplit. (Measured on 256 CUs: the bounds scale with the device's CUs.)
   const int64_t kMinWorkgroups = std::max(1, geo.cus / 4), kSplitWorkgroups = std::max(1, geo.cus / 2);
   int64_t tps = max_waves;
-  if (units * ((n_tiles + tps - 1) / tps) < kMinWorkgroups)
+  // The f32 decode kernel issues all of a wave's loads for its tile at once: a unit that its
+  // workgroup's waves cover in one round of tiles stays whole (a split would add the merge's
+  // round trips to one round of loads).
+  if (units * ((n_tiles + tps - 1) / tps) < kMinWorkgroups && !(vec && n_tiles <= max_waves))
     tps = std::max<int64_t>(1, n_tiles * units / kSplitWorkgroups);
   // a tuning knob (ffai_set_decode_tiles_per_wg / FFAI_DECODE_TILES_PER_WG) may force it
   const int forced_tps = decode_tiles_per_wg();
@@ -541,7 +556,8 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
     p.causal = d->causal; p.q_offset = d->q_offset;
     p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split; p.n_work = pl.n_work;
     p.scale_log2 = d->scale * 1.4426950408889634f;
-    const hipError_t e = ffai::launch_decode(p, mode, ot, d->head_dim, kt, pl.waves, s);
+    const hipError_t e = f32 ? ffai::launch_decode_vec(p, kvt, kt, pl.waves, s)
+                             : ffai::launch_decode(p, mode, ot, d->head_dim, kt, pl.waves, s);
     if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("decode launch: ") + hipGetErrorString(e));
     return FFAI_OK;
   }

@@ -210,6 +210,28 @@ __device__ __forceinline__ float quad_sum(float x) {
   return partner_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
 }
 
+// Max and sum over all 64 lanes, the result in every lane: within each row of 16 lanes by DPP
+// (quad permutes, then rotations by 4 and 8 lanes), then over the four rows (quad_max / quad_sum).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+  v = fmaxf(v, dpp_mov<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_mov<0x128>(v));  // row_ror:8
+  return quad_max(v);
+}
+__device__ __forceinline__ float wave_sum_all(float v) {
+  v += dpp_mov<0xb1>(v);
+  v += dpp_mov<0x4e>(v);
+  v += dpp_mov<0x124>(v);
+  v += dpp_mov<0x128>(v);
+  return quad_sum(v);
+}
+
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }

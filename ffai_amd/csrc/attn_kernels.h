@@ -108,6 +108,10 @@ hipError_t launch_fwd_f32(const FwdParams& p, int kv_dtype, int d, bool kt, int 
 // with p.n_split > 1 the unit's last workgroup merges the splits (p.counters zeroed).
 hipError_t launch_decode(const DecodeParams& p, int mode, int out_dtype, int head_dim,
                          bool k_transposed, int waves, hipStream_t stream);
+// f32 queries, one query row per (batch, kv-head) unit (group x Tq == 1), head_dim 64, K/V of
+// type kv_dtype (kF32, kF16 or kBF16), f32 output (decode_vec.hip); `waves` 1, 2, 4 or 8.
+hipError_t launch_decode_vec(const DecodeParams& p, int kv_dtype, bool k_transposed, int waves,
+                             hipStream_t stream);
 // f16 inputs (decode_f16.hip), called by launch_decode.
 hipError_t launch_decode_f16(const DecodeParams& p, int out_dtype, int head_dim,
                              bool k_transposed, int waves, hipStream_t stream);

@@ -36,6 +36,124 @@ __device__ __forceinline__ void store_row_chunk(const DecodeParams& p, int b, in
   st4<OUTT, true>(op, acc * inv);
 }
 
+// The end of a decode unit's workgroup, shared by the decode kernels: merge the NWD waves'
+// partials from LDS and write the unit's rows, or, when the unit's keys are split over
+// workgroups, this split's merged partial, and let the unit's last split merge them all.
+// LDS layout of wave w's partial (floats from mbase + w * WST): its R <= MR rows of O at
+// n * OROW, then the rows' maxima (scaled log2 units) at MR * OROW + n and weight sums at
+// MR * OROW + MR + n. Every thread of the workgroup calls it, after a barrier that publishes the
+// partials.
+template <int OUTT, int D, int NWD, int OROW, int MR, int WST>
+__device__ __forceinline__ void finish_unit(const DecodeParams& p, const float* mbase, int b,
+                                            int hk, int unit, int split, int R, int tid) {
+  constexpr int C4 = D / 4;  // 4-float chunks per row
+  const int items = R * C4;
+  const int64_t prow0 = ((int64_t)unit * p.n_split + split) * R;  // this split's first partial row
+  // the partials: O rows [units][n_split][R][D], then (m, l) pairs [units][n_split][R][2], as a
+  // buffer resource over exactly those bytes (an access past them would read 0 / be dropped)
+  const int64_t o_floats = (int64_t)p.B * p.Hkv * p.n_split * R * D;
+  const int64_t ws_bytes = (o_floats + (int64_t)p.B * p.Hkv * p.n_split * R * 2) * 4;
+  const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      p.ws, (short)0, (int)(p.n_split > 1 ? ws_bytes : 0), kBufferWord3);
+
+#pragma unroll 1
+  for (int it = tid; it < items; it += NWD * 64) {
+    const int n = it / C4, c4 = it % C4;
+    float mw[NWD];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NWD; ++w) {
+      mw[w] = mbase[w * WST + MR * OROW + n];
+      M = fmaxf(M, mw[w]);
+    }
+    const float Mc = (M == kNegInf) ? 0.f : M;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWD; ++w) {
+      const float* mb = mbase + w * WST;
+      const float wt = fast_exp2(mw[w] - Mc);  // 0 for an empty wave (m = -inf)
+      acc += wt * *reinterpret_cast<const f32x4*>(&mb[n * OROW + 4 * c4]);
+      L = __builtin_fmaf(wt, mb[MR * OROW + MR + n], L);
+    }
+    if (p.n_split == 1) {
+      store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
+    } else {
+      // This split's partial, written with device-scope (sc1) buffer stores: each one reaches
+      // the device's coherence point before it is acknowledged, so the unit's last workgroup
+      // reads it wherever (on whichever XCD) it runs, without a write-back of this L2's dirty
+      // lines.
+      __builtin_amdgcn_raw_buffer_store_b128(acc, ws_rsrc, (int)(((prow0 + n) * D + 4 * c4) * 4),
+                                             0, kDeviceScope);
+      if (c4 == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(f32x2{M, L}, ws_rsrc,
+                                              (int)((o_floats + (prow0 + n) * 2) * 4), 0,
+                                              kDeviceScope);
+    }
+  }
+  if (p.n_split == 1) return;
+
+  // ---- count this split; the unit's last one merges them all.
+  // Ordering: every thread waits for its partial stores to be acknowledged (vmcnt(0): device-
+  // scope stores are acknowledged once they are visible at device scope), the barrier makes that
+  // true of the whole workgroup, and only then does one thread add 1 to the unit's counter (a
+  // device-scope atomic). The workgroup that reads n_split - 1 back is the unit's last: every
+  // other split's partial was visible before its increment, which precedes this one in the
+  // counter's order, and this workgroup's device-scope loads are issued after that increment
+  // returns. The last workgroup sets the counter back to 0 for the next call (no wait anywhere:
+  // a workgroup that is not last simply ends).
+  __shared__ int s_last;
+  vm_wait_all();
+  __syncthreads();
+  if (tid == 0) {
+    const int done = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (done == p.n_split - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int S = p.n_split;
+  const int64_t uo = (int64_t)unit * S * R * D;               // the unit's first O row (floats)
+  const int64_t uml = o_floats + (int64_t)unit * S * R * 2;   // and its first (m, l) pair
+  // Online log-sum-exp merge over the splits, eight at a time: the eight splits' device-scope
+  // loads are issued together (clamped to the last split; those past it count as empty), then
+  // merged in split order, so one round trip covers eight partials. (Sixteen at a time measured
+  // slower at 8 and 12 splits: the unrolled merge doubles the code a cold workgroup fetches.)
+  constexpr int KS = 8;
+#pragma unroll 1
+  for (int it = tid; it < items; it += NWD * 64) {
+    const int n = it / C4, c4 = it % C4;
+    float M = kNegInf, L = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int s0 = 0; s0 < S; s0 += KS) {
+      f32x2 mlj[KS];
+      f32x4 xj[KS];
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const int row = min(s0 + j, S - 1) * R + n;
+        mlj[j] = __builtin_amdgcn_raw_buffer_load_b64(ws_rsrc, (int)((uml + row * 2) * 4), 0,
+                                                      kDeviceScope);
+        xj[j] = __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, (int)((uo + row * D + 4 * c4) * 4),
+                                                      0, kDeviceScope);
+      }
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const float m = (s0 + j < S) ? mlj[j][0] : kNegInf;
+        const float m_new = fmaxf(M, m);
+        if (m_new == kNegInf) continue;  // nothing seen yet (every key so far masked)
+        const float c_old = fast_exp2(M - m_new);  // 0 while M is -inf
+        const float c_new = fast_exp2(m - m_new);  // 0 for an empty split
+        acc = acc * c_old + xj[j] * c_new;
+        L = L * c_old + mlj[j][1] * c_new;
+        M = m_new;
+      }
+    }
+    store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // NC: 16-column blocks of query rows (1 for units of at most 16 rows, 2 for up to 32).
 template <int MODE, int OUTT, int D, bool KT, int NWD, int NC>
 __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
@@ -459,112 +577,255 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  constexpr int C4 = D / 4;  // 4-float chunks per row
-  const int items = R * C4;
-  const int64_t prow0 = ((int64_t)unit * p.n_split + split) * R;  // this split's first partial row
-  // the partials: O rows [units][n_split][R][D], then (m, l) pairs [units][n_split][R][2], as a
-  // buffer resource over exactly those bytes (an access past them would read 0 / be dropped)
-  const int64_t o_floats = (int64_t)p.B * p.Hkv * p.n_split * R * D;
-  const int64_t ws_bytes = (o_floats + (int64_t)p.B * p.Hkv * p.n_split * R * 2) * 4;
-  const __amdgpu_buffer_rsrc_t ws_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      p.ws, (short)0, (int)(p.n_split > 1 ? ws_bytes : 0), kBufferWord3);
+  finish_unit<OUTT, D, NWD, OROW, 32, WBUF / 2>(p, mbase, b, hk, unit, split, R, tid);
+}
 
+
+// ---------------------------------------------------------------------------------------------
+// f32 queries, one query row per (batch, kv-head) unit, head_dim 64: the reference's own decode
+// arms, a query row in f32 over f16 K/V (flash_attn.rs:289-356, xattn_head_f16 :698-789: the
+// cross-attention cache) or f32 K/V (:370-399, xattn_head :595-696: the self-attention cache),
+// and bf16 K/V alike. With one row the two products are matrix-vector products: an MFMA would
+// compute 16 columns to keep one, so this kernel runs them on the VALU in f32, reading K and V
+// straight into registers with 16-byte (8-byte for 16-bit K^T) vector loads, every load of a
+// wave's 64-key tile in flight at once (24 or 32 loads per lane, under the 63 a wave can have
+// outstanding):
+//   * scores: lane (kq, dg) = (lane % 16, lane / 16) takes keys 4 kq .. 4 kq + 3 over head dims
+//     16 dg .. 16 dg + 15: K^T (the reference's layout) as 4-key chunks of 16 d-rows, K as rows
+//     as 16-d slices of 4 rows. The four d-groups' partial dot products are summed across the
+//     lane groups (v_permlane16/32_swap), so every lane holds its 4 keys' full scores;
+//   * softmax: online over the wave's tiles, in base 2 with v_exp_f32; the tile max over the 16
+//     lanes of a row by DPP;
+//   * PV: the weights go through a 256-byte LDS slot of the wave; lane (c, g) takes a 16-byte
+//     chunk c of the V rows (4 f32 or 8 16-bit elements of d) for the rows of group g, and the
+//     groups' partial outputs are summed at the end.
+// Waves take their own 64-key tiles and merge through LDS; split units merge as in
+// decode_kernel (finish_unit). The host launches it for f32 queries, group x q_len == 1,
+// head_dim 64, 4-element-aligned operands, and heads whose K and V lie within 2^31 bytes.
+template <int KVT, bool KT, int NWD>
+__global__ __launch_bounds__(NWD * 64) void decode_vec_kernel(DecodeParams p) {
+  constexpr int D = 64;
+  constexpr int OROW = D + 4;     // merge area of a wave: its O row,
+  constexpr int WST = OROW + 4;   // then its max and weight sum (16-byte aligned stride)
+  using KVS = store_t<KVT>;
+  constexpr int ES = (int)sizeof(KVS);
+  constexpr int VE = 16 / ES;        // V elements per 16-byte chunk: 4 (f32) or 8 (16-bit)
+  constexpr int VC = D / VE;         // chunks per V row: lanes per row group
+  constexpr int VG = 64 / VC;        // row groups: 4 (f32) or 8 (16-bit)
+  constexpr int VR = BN / VG;        // rows per group: 16 or 8
+  using KR = std::conditional_t<KVT == kF32, f32x4, u32x2>;  // 4 K elements as loaded
+  __shared__ __attribute__((aligned(16))) float mlds[NWD * WST];
+  __shared__ __attribute__((aligned(16))) float wlds[NWD * BN];  // each wave's tile weights
+
+  const int split = wg_id_x();
+  const int hk = wg_id_y();
+  const int b = wg_id_z();
+  const int unit = b * p.Hkv + hk;
+  const int tid = item_id();
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kq = lane & 15, dg = lane >> 4;  // scores: keys 4 kq + e, d in [16 dg, 16 dg + 16)
+  const int vc = lane % VC, vg = lane / VC;  // PV: chunk vc of d, rows VR vg .. VR vg + VR - 1
+
+  int kv_end = p.Tk;
+  if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
+  kv_end = __builtin_amdgcn_readfirstlane(kv_end);  // uniform (one batch item per workgroup)
+  // the row's last visible key (q_len 1: the row's position is q_offset)
+  const int lim = p.causal ? min(kv_end - 1, p.q_offset) : kv_end - 1;
+  const int n_tiles = (max(0, lim + 1) + BN - 1) / BN;
+  const int t_begin = split * p.tiles_per_split;
+  const int t_end = min(n_tiles, t_begin + p.tiles_per_split);
+  const float sl2 = p.scale_log2;
+
+  const KVS* kp = reinterpret_cast<const KVS*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const KVS* vp = reinterpret_cast<const KVS*>(p.v) + b * p.v_sb + hk * p.v_sh;
+  // this lane's 16 query elements, d = 16 dg .. 16 dg + 15 (head hk * group, position 0)
+  const float* qr =
+      reinterpret_cast<const float*>(p.q) + b * p.q_sb + (int64_t)hk * p.group * p.q_sh + 16 * dg;
+  float q[16];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(qr + 4 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[4 * c + e] = x[e];
+  }
+  // K and V are read at 32-bit byte offsets from the head's base, stepped in vector registers
+  // (an empty asm after each step keeps the compiler from hoisting 16 row offsets per operand
+  // into scalar registers)
+  const char* kb8 = reinterpret_cast<const char*>(kp);
+  const char* vb8 = reinterpret_cast<const char*>(vp);
+  const uint32_t kstep = (uint32_t)p.k_st * (uint32_t)ES;
+  const uint32_t vstep = (uint32_t)p.v_st * (uint32_t)ES;
+  float* wl = wlds + wave * BN;
+
+  f32x4 o4[VE / 4];      // this lane's partial O over its row group, d = VE vc ..
+#pragma unroll
+  for (int i = 0; i < VE / 4; ++i) o4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_s = kNegInf;   // running max, scaled log2 units (wave-uniform)
+  float l_run = 0.f;     // running weight sum of this lane's 4 keys
 #pragma unroll 1
-  for (int it = tid; it < items; it += NWD * 64) {
-    const int n = it / C4, c4 = it % C4;
-    float mw[NWD];
-    float M = kNegInf;
+  for (int it = t_begin + wave; it < t_end; it += NWD) {
+    const int kb = it * BN;
+    const int k0 = kb + 4 * kq;  // this lane's first key
+    // ---- loads, as raw bits (widened after every load is issued): K (4 keys x 16 d) and V
+    //      (VR rows x one 16-byte chunk)
+    KR kraw[16];  // K^T layout: element e of kraw[i] = K(key k0 + e, d = 16 dg + i);
+                  // rows: element e of kraw[4 r + c] = K(key k0 + r, d = 16 dg + 4 c + e)
+    if constexpr (KT) {
+      // a chunk wholly past the operand's end reads the row's first chunk instead (its keys
+      // are masked); only a chunk that straddles the end goes element by element
+      const int kc0 = k0 < p.Tk ? k0 : 0;
+      uint32_t off = ((uint32_t)(16 * dg) * (uint32_t)p.k_st + (uint32_t)kc0) * ES;
+      if (kc0 + 4 <= p.Tk) {
 #pragma unroll
-    for (int w = 0; w < NWD; ++w) {
-      mw[w] = mbase[w * (WBUF / 2) + 32 * OROW + n];
-      M = fmaxf(M, mw[w]);
-    }
-    const float Mc = (M == kNegInf) ? 0.f : M;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float L = 0.f;
+        for (int i = 0; i < 16; ++i) {
+          kraw[i] = *reinterpret_cast<const KR*>(kb8 + off);
+          off += kstep;
+          asm volatile("" : "+v"(off));
+        }
+      } else {
+        // the chunk holding the operand's last key (or an operand of fewer than 4 keys):
+        // elements clamped to the last key
+        const int cl = max(0, min(3, p.Tk - 1 - kc0));
+        uint32_t off0 = off;
 #pragma unroll
-    for (int w = 0; w < NWD; ++w) {
-      const float* mb = mbase + w * (WBUF / 2);
-      const float wt = fast_exp2(mw[w] - Mc);  // 0 for an empty wave (m = -inf)
-      acc += wt * *reinterpret_cast<const f32x4*>(&mb[n * OROW + 4 * c4]);
-      L = __builtin_fmaf(wt, mb[32 * OROW + 32 + n], L);
-    }
-    if (p.n_split == 1) {
-      store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
+        for (int i = 0; i < 16; ++i) {
+          const KVS* r = reinterpret_cast<const KVS*>(kb8 + off0);
+          if constexpr (KVT == kF32) {
+            kraw[i] = f32x4{r[0], r[min(1, cl)], r[min(2, cl)], r[min(3, cl)]};
+          } else {
+            kraw[i] = u32x2{(uint32_t)r[0] | ((uint32_t)r[min(1, cl)] << 16),
+                            (uint32_t)r[min(2, cl)] | ((uint32_t)r[min(3, cl)] << 16)};
+          }
+          off0 += kstep;
+          asm volatile("" : "+v"(off0));
+        }
+      }
     } else {
-      // This split's partial, written with device-scope (sc1) buffer stores: each one reaches
-      // the device's coherence point before it is acknowledged, so the unit's last workgroup
-      // reads it wherever (on whichever XCD) it runs, without a write-back of this L2's dirty
-      // lines.
-      __builtin_amdgcn_raw_buffer_store_b128(acc, ws_rsrc, (int)(((prow0 + n) * D + 4 * c4) * 4),
-                                             0, kDeviceScope);
-      if (c4 == 0)
-        __builtin_amdgcn_raw_buffer_store_b64(f32x2{M, L}, ws_rsrc,
-                                              (int)((o_floats + (prow0 + n) * 2) * 4), 0,
-                                              kDeviceScope);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const KVS* kr = kp + (int64_t)min(k0 + r, kv_end - 1) * p.k_st + 16 * dg;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kraw[4 * r + c] = *reinterpret_cast<const KR*>(kr + 4 * c);
+      }
     }
-  }
-  if (p.n_split == 1) return;
+    u32x4 vx[VR];  // row VR vg + i, elements VE vc .. VE vc + VE - 1 (raw bits)
+    {
+      const int r0 = kb + VR * vg;
+      uint32_t off = ((uint32_t)r0 * (uint32_t)p.v_st + (uint32_t)(VE * vc)) * ES;
+      if (kb + BN <= kv_end) {
+#pragma unroll
+        for (int i = 0; i < VR; ++i) {
+          vx[i] = ld16(vb8 + off);
+          off += vstep;
+          asm volatile("" : "+v"(off));
+        }
+      } else {
+        // the last tile: rows past the last valid one read that row (their weights are 0)
+#pragma unroll
+        for (int i = 0; i < VR; ++i) {
+          const uint32_t row = (uint32_t)min(r0 + i, kv_end - 1);
+          vx[i] = ld16(vb8 + (row * (uint32_t)p.v_st + (uint32_t)(VE * vc)) * ES);
+        }
+      }
+    }
+    // every load of the tile is issued before the first product waits for one
+    __builtin_amdgcn_sched_barrier(0);
 
-  // ---- count this split; the unit's last one merges them all.
-  // Ordering: every thread waits for its partial stores to be acknowledged (vmcnt(0): device-
-  // scope stores are acknowledged once they are visible at device scope), the barrier makes that
-  // true of the whole workgroup, and only then does one thread add 1 to the unit's counter (a
-  // device-scope atomic). The workgroup that reads n_split - 1 back is the unit's last: every
-  // other split's partial was visible before its increment, which precedes this one in the
-  // counter's order, and this workgroup's device-scope loads are issued after that increment
-  // returns. The last workgroup sets the counter back to 0 for the next call (no wait anywhere:
-  // a workgroup that is not last simply ends).
-  __shared__ int s_last;
-  vm_wait_all();
-  __syncthreads();
-  if (tid == 0) {
-    const int done = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (done == p.n_split - 1) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  const int S = p.n_split;
-  const int64_t uo = (int64_t)unit * S * R * D;               // the unit's first O row (floats)
-  const int64_t uml = o_floats + (int64_t)unit * S * R * 2;   // and its first (m, l) pair
-  // Online log-sum-exp merge over the splits, eight at a time: the eight splits' device-scope
-  // loads are issued together (clamped to the last split; those past it count as empty), then
-  // merged in split order, so one round trip covers eight partials. (Sixteen at a time measured
-  // slower at 8 and 12 splits: the unrolled merge doubles the code a cold workgroup fetches.)
-  constexpr int KS = 8;
-#pragma unroll 1
-  for (int it = tid; it < items; it += NWD * 64) {
-    const int n = it / C4, c4 = it % C4;
-    float M = kNegInf, L = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-    for (int s0 = 0; s0 < S; s0 += KS) {
-      f32x2 mlj[KS];
-      f32x4 xj[KS];
+    f32x4 kx[16];
 #pragma unroll
-      for (int j = 0; j < KS; ++j) {
-        const int row = min(s0 + j, S - 1) * R + n;
-        mlj[j] = __builtin_amdgcn_raw_buffer_load_b64(ws_rsrc, (int)((uml + row * 2) * 4), 0,
-                                                      kDeviceScope);
-        xj[j] = __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, (int)((uo + row * D + 4 * c4) * 4),
-                                                      0, kDeviceScope);
-      }
-#pragma unroll
-      for (int j = 0; j < KS; ++j) {
-        const float m = (s0 + j < S) ? mlj[j][0] : kNegInf;
-        const float m_new = fmaxf(M, m);
-        if (m_new == kNegInf) continue;  // nothing seen yet (every key so far masked)
-        const float c_old = fast_exp2(M - m_new);  // 0 while M is -inf
-        const float c_new = fast_exp2(m - m_new);  // 0 for an empty split
-        acc = acc * c_old + xj[j] * c_new;
-        L = L * c_old + mlj[j][1] * c_new;
-        M = m_new;
+    for (int i = 0; i < 16; ++i) {
+      if constexpr (KVT == kF32) {
+        kx[i] = kraw[i];
+      } else {
+        kx[i] = f32x4{to_f32<KVT>(kraw[i].x & 0xffffu), to_f32<KVT>(kraw[i].x >> 16),
+                      to_f32<KVT>(kraw[i].y & 0xffffu), to_f32<KVT>(kraw[i].y >> 16)};
       }
     }
-    store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
+    // ---- scores of keys k0 .. k0 + 3: this lane's 16 d, then summed over the 4 d-groups
+    float sc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float kv = KT ? kx[i][e] : kx[4 * e + i / 4][i % 4];
+        a = __builtin_fmaf(q[i], kv, a);
+      }
+      sc[e] = quad_sum(a);
+    }
+    float tmax = kNegInf;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sc[e] = (k0 + e <= lim) ? sc[e] * sl2 : kNegInf;
+      tmax = fmaxf(tmax, sc[e]);
+    }
+    tmax = fmaxf(tmax, dpp_mov<0xb1>(tmax));   // max over the row's 16 lanes
+    tmax = fmaxf(tmax, dpp_mov<0x4e>(tmax));
+    tmax = fmaxf(tmax, dpp_mov<0x124>(tmax));
+    tmax = fmaxf(tmax, dpp_mov<0x128>(tmax));
+    // the tile's first key is visible, so the max is finite from the first tile on
+    const float m_new = fmaxf(m_s, tmax);
+    const float corr = (m_new == m_s) ? 1.f : fast_exp2(m_s - m_new);
+    m_s = m_new;
+    f32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = fast_exp2(sc[e] - m_new);  // 0 for a masked key
+    l_run = __builtin_fmaf(l_run, corr, (w[0] + w[1]) + (w[2] + w[3]));
+    // ---- weights through LDS (the wave's own slot: ordering within the wave only)
+    if (dg == 0) *reinterpret_cast<f32x4*>(&wl[4 * kq]) = w;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot is written
+    f32x4 wr[VR / 4];
+#pragma unroll
+    for (int i = 0; i < VR / 4; ++i) wr[i] = *reinterpret_cast<const f32x4*>(&wl[VR * vg + 4 * i]);
+    // ---- O += w V over this lane's rows
+#pragma unroll
+    for (int c = 0; c < VE / 4; ++c) o4[c] *= corr;
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      const float wi = wr[i / 4][i % 4];
+      if constexpr (KVT == kF32) {
+        o4[0] += wi * __builtin_bit_cast(f32x4, vx[i]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < VE / 4; ++c) {
+          const f32x4 v = {to_f32<KVT>(vx[i][2 * c] & 0xffffu), to_f32<KVT>(vx[i][2 * c] >> 16),
+                           to_f32<KVT>(vx[i][2 * c + 1] & 0xffffu),
+                           to_f32<KVT>(vx[i][2 * c + 1] >> 16)};
+          o4[c] += wi * v;
+        }
+      }
+    }
+    // the slot is rewritten by the next tile: its reads must be done (LDS returns in order)
+    __builtin_amdgcn_s_waitcnt(0xc07f);
   }
-  if (tid == 0) __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- this wave's partial to LDS (a wave without tiles leaves m = -inf, l = 0, O = 0): O
+  // summed over the row groups (lanes vc + VC g), l over the 16 lanes of a row
+  float l_tot = l_run;
+  l_tot += dpp_mov<0xb1>(l_tot);
+  l_tot += dpp_mov<0x4e>(l_tot);
+  l_tot += dpp_mov<0x124>(l_tot);
+  l_tot += dpp_mov<0x128>(l_tot);
+#pragma unroll
+  for (int c = 0; c < VE / 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = o4[c][e];
+      if constexpr (VG == 8) x += dpp_mov<0x128>(x);  // lanes l and l ^ 8 (row_ror:8)
+      o4[c][e] = quad_sum(x);
+    }
+  float* mb = mlds + wave * WST;
+  if (vg == 0) {
+#pragma unroll
+    for (int c = 0; c < VE / 4; ++c) *reinterpret_cast<f32x4*>(&mb[VE * vc + 4 * c]) = o4[c];
+  }
+  if (lane == 0) {
+    mb[OROW] = m_s;
+    mb[OROW + 1] = l_tot;
+  }
+  __syncthreads();
+  finish_unit<kF32, D, NWD, OROW, 1, WST>(p, mlds, b, hk, unit, split, 1, tid);
 }
 
 }  // namespace

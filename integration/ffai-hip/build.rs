@@ -6,8 +6,9 @@
 use std::path::{Path, PathBuf};
 use std::process::Command;
 
-const SOURCES: [&str; 11] = [
-    "fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "decode_f16.hip", "kv_cache.hip",
+const SOURCES: [&str; 12] = [
+    "fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "decode_f16.hip", "decode_vec.hip",
+    "kv_cache.hip",
     "gemv.hip", "probe.hip", "attn_launch.hip", "attn_api.cpp", "encoder_attn.cpp",
 ];
 

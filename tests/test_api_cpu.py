@@ -423,6 +423,17 @@ def _plan(lib, *args, causal=0):
     # beam-5 cross-attention: the decode kernel, 8 pieces of 3 tiles per head (128 workgroups)
     ((L.BF16, L.BF16, L.F32, 1, 16, 16, 5, 1500, 64, L.K_TRANSPOSED), 0,
      [1, 4, 8, 3, 128], [0, 0, 0]),
+    # the reference's cross-attention arm (one beam: f32 q, f16 K^T/V, 1500 frames, 16 heads):
+    # the f32 decode kernel, 8 pieces of 3 tiles per head
+    ((L.F32, L.F16, L.F32, 1, 16, 16, 1, 1500, 64, L.K_TRANSPOSED), 0,
+     [1, 4, 8, 3, 128], [0, 0, 0]),
+    # its self-attention arm (f32 q and K^T/V, 448 cached positions): one workgroup of 8 waves per
+    # head covers the 7 tiles in one round of loads, unsplit
+    ((L.F32, L.F32, L.F32, 1, 16, 16, 1, 448, 64, L.K_TRANSPOSED), 0,
+     [1, 8, 1, 7, 16], [0, 0, 0]),
+    # five beams' f32 self-attention in one call (80 units)
+    ((L.F32, L.F32, L.F32, 5, 16, 16, 1, 448, 64, L.K_ROWS), 0,
+     [1, 8, 1, 7, 80], [0, 0, 0]),
 ])
 def test_plans_of_the_benchmarked_workloads(lib, args, causal, info, splits):
     got_info, got_splits = _plan(lib, *args, causal=causal)
