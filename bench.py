@@ -19,7 +19,8 @@ bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras] [--eager]
                        [--layers L]
-                       [--legs decode,state,block,gemv,tiny,small,prefill,floor,pipes | none | copy]
+                       [--legs decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes
+                               | none | copy]
 """
 
 from __future__ import annotations
@@ -48,9 +49,11 @@ def parse():
     ap.add_argument("--eager", action="store_true",
                     help="decode leg without HIP graphs (for counter collection)")
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--legs", default="decode,state,block,gemv,tiny,small,prefill,floor,pipes",
+    ap.add_argument("--legs",
+                    default="decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "state, block, gemv, tiny, small, prefill, floor, pipes, or 'none'; "
+                         "decode_ref, state, block, gemv, tiny, small, prefill, floor, pipes, or "
+                         "'none'; "
                          "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
@@ -341,6 +344,127 @@ def decode_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=
         "mean_self_len": float(lens_cpu.float().mean()),
         "buffer_sets": sets,
         "hip_graphs": graphs,
+    }
+
+
+def decode_ref_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, cap=448,
+                     layers=24, sets=3):
+    """The beam-5 whisper-medium decode step as the reference calls its kernel: per layer and per
+    beam, one after another (decoder.rs:542-596), the self-attention arm (f32 q over that beam's
+    f32 K^T/V cache, flash_attn.rs:370-399) and the cross-attention arm (f32 q over the window's
+    f16 K^T/V, :289-356; text_decoder.rs:771-793), each one call of ffai_attn_fwd on the f32
+    decode kernel: 2 x 5 x 24 = 240 launches per step in HIP graphs, 3 buffer sets beyond the
+    MALL. Cache lengths are the 16-bit decode leg's (seed 3). Besides the step, graphs of the
+    cross-attention calls alone and of the self-attention calls alone give per-launch times, and
+    one more times each layer's five self-attention calls as one call over the 5 beams (batch 5,
+    ragged lengths), the comparison at the bytes per launch of the 16-bit beam kernel."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device="cpu").manual_seed(3)
+    lens_cpu = torch.randint(1, cap + 1, (layers, beams), generator=g, dtype=torch.int32)
+    gd = torch.Generator(device=dev).manual_seed(31)
+    scale = D ** -0.5
+    all_sets = []
+    for _ in range(sets):
+        layer_bufs = []
+        for l in range(layers):
+            kt_s = torch.randn(beams, H, D, cap, generator=gd, device=dev)
+            v_s = torch.randn(beams, H, cap, D, generator=gd, device=dev)
+            q_s = torch.randn(beams, H, 1, D, generator=gd, device=dev)
+            q_x = torch.randn(beams, H, 1, D, generator=gd, device=dev)
+            kt_x = torch.randn(1, H, D, T_enc, generator=gd, device=dev).half()
+            v_x = torch.randn(1, H, T_enc, D, generator=gd, device=dev).half()
+            o_s = torch.empty(beams, H, 1, D, device=dev)
+            o_x = torch.empty(beams, H, 1, D, device=dev)
+            calls_s, calls_x = [], []
+            for b in range(beams):
+                n = int(lens_cpu[l, b])
+                calls_s.append((q_s[b:b + 1], kt_s[b:b + 1, :, :, :n], v_s[b:b + 1, :, :n],
+                                o_s[b:b + 1]))
+                calls_x.append((q_x[b:b + 1], kt_x, v_x, o_x[b:b + 1]))
+            # the same self-attention as one call over the 5 beams (ragged lengths)
+            batched = (q_s, kt_s, v_s, o_s, lens_cpu[l].to(dev))
+            layer_bufs.append((calls_s, calls_x, batched))
+        all_sets.append(layer_bufs)
+    # workspaces (one per call site, reused: calls are stream-ordered), for the largest need
+    c_x = all_sets[0][0][1][0]
+    ws_x = torch.zeros(max(16, fa.workspace_bytes(*c_x, k_transposed=True, scale=scale)),
+                       dtype=torch.uint8, device=dev)
+    ws_s = torch.zeros(max(16, max(fa.workspace_bytes(*c, k_transposed=True, scale=scale)
+                                   for lb in all_sets[0] for c in lb[0])),
+                       dtype=torch.uint8, device=dev)
+    qb, ktb, vb, ob, lb0 = all_sets[0][0][2]
+    ws_b = torch.zeros(max(16, fa.workspace_bytes(qb, ktb, vb, ob, k_transposed=True, scale=scale,
+                                                  kv_lens=lb0)), dtype=torch.uint8, device=dev)
+    longest = max((c for lb in all_sets[0] for c in lb[0]), key=lambda c: c[1].shape[3])
+    plans = {"cross": fa.plan(*c_x, k_transposed=True, scale=scale),
+             f"self_{longest[1].shape[3]}": fa.plan(*longest, k_transposed=True, scale=scale)}
+
+    def step(layer_bufs, which):
+        for calls_s, calls_x, (qb, ktb, vb, ob, lb) in layer_bufs:
+            if which == "self_batched":
+                fa.attention(qb, ktb, vb, k_transposed=True, scale=scale, kv_lens=lb, out=ob,
+                             workspace=ws_b)
+                continue
+            for b in range(beams):
+                if which in ("both", "self"):
+                    q, kt, v, o = calls_s[b]
+                    fa.attention(q, kt, v, k_transposed=True, scale=scale, out=o, workspace=ws_s)
+                if which in ("both", "cross"):
+                    q, kt, v, o = calls_x[b]
+                    fa.attention(q, kt, v, k_transposed=True, scale=scale, out=o, workspace=ws_x)
+
+    def timed(which):
+        step(all_sets[0], which)
+        torch.cuda.synchronize()
+        captured = []
+        for s_ in range(sets):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step(all_sets[s_], which)
+            captured.append(gr)
+        torch.cuda.synchronize()
+        for i in range(warmup):
+            captured[i % sets].replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            captured[i % sets].replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    us_step = timed("both")
+    us_cross = timed("cross")
+    us_self = timed("self")
+    us_self_b = timed("self_batched")
+    n_calls = layers * beams
+    qo = H * D * 4 * 2                                    # f32 q read, f32 out written
+    cross_call = H * T_enc * D * 2 * 2 + qo               # f16 K^T + V of the window
+    self_bytes = int(lens_cpu.sum()) * H * D * 4 * 2 + n_calls * qo
+    step_bytes = n_calls * cross_call + self_bytes
+    return {
+        "us_per_step": us_step,
+        "bytes_per_step": step_bytes,
+        "gbps": step_bytes / (us_step * 1e-6) / 1e9,
+        "hbm_frac": step_bytes / (us_step * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+        "launches_per_step": 2 * n_calls,
+        "cross_us_per_launch": us_cross / n_calls,
+        "cross_bytes_per_launch": cross_call,
+        "cross_gbps_per_launch": cross_call / (us_cross / n_calls * 1e-6) / 1e9,
+        "self_us_per_launch": us_self / n_calls,
+        "self_mean_bytes_per_launch": self_bytes / n_calls,
+        "self_gbps_per_launch": self_bytes / (us_self * 1e-6) / 1e9,
+        "self_batched_us_per_launch": us_self_b / layers,
+        "self_batched_gbps_per_launch": self_bytes / (us_self_b * 1e-6) / 1e9,
+        "mean_self_len": float(lens_cpu.float().mean()),
+        "plans": plans,
+        "buffer_sets": sets,
+        "hip_graphs": True,
+        "note": ("bytes count each call's reads as the reference issues them: the cross K/V "
+                 "once per beam"),
     }
 
 
@@ -853,6 +977,16 @@ def main():
         dec = decode_bench(torch, fa, max(args.steps * 10, 100), 10, graphs=not args.eager)
         log(f"decode: {dec['us_per_step']:.1f} us/step, {dec['gbps']:.0f} GB/s")
         extras["decode_beam5"] = dec
+    if "decode_ref" in legs:
+        log("decode, the reference's calls: per beam, f32 q over f32 self / f16 cross caches ...")
+        dr = decode_ref_bench(torch, fa, max(args.steps * 2, 20), 3)
+        log(f"decode (reference calls): {dr['us_per_step']:.1f} us/step ({dr['gbps']:.0f} GB/s); "
+            f"cross {dr['cross_us_per_launch']:.2f} us/launch ({dr['cross_gbps_per_launch']:.0f} "
+            f"GB/s), self {dr['self_us_per_launch']:.2f} us/launch "
+            f"({dr['self_gbps_per_launch']:.0f} GB/s), self 5 beams per call "
+            f"{dr['self_batched_us_per_launch']:.2f} us/launch "
+            f"({dr['self_batched_gbps_per_launch']:.0f} GB/s)")
+        extras["decode_ref_beam5"] = dr
     if "state" in legs:
         log("decode state: append + beam reorder, whisper-medium ...")
         st = decode_state_bench(torch, fa, 100, 10)
