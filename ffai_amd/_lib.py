@@ -124,6 +124,9 @@ def load():
     L.ffai_set_decode_tiles_per_wg.argtypes = [ctypes.c_int]
     L.ffai_set_decode_tiles_per_wg.restype = None
     L.ffai_attn_plan_splits.argtypes = [dp, ctypes.POINTER(ctypes.c_int32)]
+    L.ffai_set_attn_variant.argtypes = [ctypes.c_int]
+    L.ffai_set_attn_variant.restype = None
+    L.ffai_get_attn_variant.restype = ctypes.c_int
     L.ffai_set_geometry_override.argtypes = [ctypes.c_int, ctypes.c_int]
     L.ffai_set_geometry_override.restype = None
     L.ffai_set_fwd_split_override.argtypes = [ctypes.c_int, ctypes.c_int]
@@ -170,7 +173,7 @@ def plan_info(desc: AttnDesc) -> dict:
     info = (ctypes.c_int32 * 5)()
     check(load().ffai_attn_plan_info(ctypes.byref(desc), info))
     kernel = "decode" if info[0] == 1 else "fwd"
-    shape = info[1] if kernel == "decode" else ("wave1", "wave4", "wave4x2")[info[1]]
+    shape = info[1] if kernel == "decode" else ("wave1", "wave4", "wave4x2", "wave4x2x16")[info[1]]
     out = {"kernel": kernel, "shape": shape, "splits": info[2], "tiles_per_split": info[3],
            "workgroups": info[4]}
     sp = (ctypes.c_int32 * 3)()

@@ -139,6 +139,23 @@ int decode_tiles_per_wg() {
   return v;
 }
 
+// Tuning knob, no counterpart in the reference: a forced launch shape of the fused kernel (-1:
+// the planner's choice). Initialised from FFAI_ATTN_VARIANT on first use.
+std::atomic<int> g_attn_variant{-2};
+
+int attn_variant() {
+  int v = g_attn_variant.load(std::memory_order_relaxed);
+  if (v == -2) {
+    int init = -1;
+    if (const char* e = std::getenv("FFAI_ATTN_VARIANT"))
+      if (e[0] >= '0' && e[0] <= '3' && e[1] == '\0') init = e[0] - '0';
+    int expected = -2;
+    g_attn_variant.compare_exchange_strong(expected, init, std::memory_order_relaxed);
+    v = g_attn_variant.load(std::memory_order_relaxed);
+  }
+  return v;
+}
+
 constexpr int kMinSeq = 256;  // flash_attn.rs:55 (MIN_SEQ)
 constexpr int kHD = 64;       // flash_attn.rs:50
 
@@ -210,6 +227,7 @@ struct Plan {
   // fwd: items [split_lo, split_hi) of n_items run as n_split pieces; dispatch sections
   int n_items, split_lo, split_hi, sec1_work;
   bool xcd_remap;
+  bool x16;       // the four-wave x 64-row shape runs on fwd16_kernel (16x16x32 MFMA)
   int xcd_shift;  // log2 of the XCDs the sections are rounded to (0: one)
   int cus;
   size_t ws_bytes;
@@ -325,14 +343,17 @@ Plan make_plan(const ffai_attn_desc* d, bool allow_split, bool vector_ok,
   // bf16: 42.5 against 69.7 us; whisper-tiny f32: 66 against 154 us).
   if (p.variant == ffai::kWave4 && work_of(p.variant) < cus && !f32 && d->q_len < 256)
     p.variant = ffai::kWave1;
-  // FFAI_ATTN_VARIANT (0, 1, 2) forces a launch shape where it is instantiated: a tuning knob.
-  static const int forced = [] {
-    const char* e = std::getenv("FFAI_ATTN_VARIANT");
-    return (e && e[0] >= '0' && e[0] <= '2' && e[1] == '\0') ? e[0] - '0' : -1;
-  }();
+  // A forced launch shape (ffai_set_attn_variant, initialised from FFAI_ATTN_VARIANT: 0, 1, 2
+  // or 3) where it is instantiated: a tuning knob. 3 is the four-wave x 64-row shape on
+  // fwd16_kernel (16x16x32 MFMA), which measured 2-4% slower than fwd_kernel's and is not
+  // chosen otherwise.
+  const int forced = attn_variant();
+  p.x16 = false;
   if (forced == ffai::kWave1 || forced == ffai::kWave4 ||
-      (forced == ffai::kWave4x2 && !f32 && d->head_dim == 64))
-    p.variant = forced;
+      ((forced == ffai::kWave4x2 || forced == ffai::kWave4x2x16) && !f32 && d->head_dim == 64)) {
+    p.variant = forced == ffai::kWave4x2x16 ? ffai::kWave4x2 : forced;
+    p.x16 = forced == ffai::kWave4x2x16;
+  }
   const int64_t items = work_of(p.variant);
   const int bm = ffai::block_m_of(p.variant);
   p.n_qblk = (d->q_len + bm - 1) / bm;
@@ -593,7 +614,8 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
             int64_t(ffai::kBlockN) * d->v_strides[2] * 2 < lim;
   }
   p.scale_log2 = d->scale * 1.4426950408889634f;
-  const hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt, pl.variant, s);
+  const hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt,
+                                        pl.x16 ? ffai::kWave4x2x16 : pl.variant, s);
   if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));
   return FFAI_OK;
 }
@@ -738,7 +760,7 @@ int ffai_attn_plan_info(const ffai_attn_desc* d, int32_t info[5]) {
   if (rc != FFAI_OK) return fail(rc, why);
   const Plan p = make_plan(d, true, true);
   info[0] = p.decode ? 1 : 0;
-  info[1] = p.decode ? p.waves : p.variant;
+  info[1] = p.decode ? p.waves : (p.x16 ? ffai::kWave4x2x16 : p.variant);
   info[2] = p.n_split;
   info[3] = p.tiles_per_split;
   info[4] = p.n_work;
@@ -754,7 +776,7 @@ int ffai_attn_noalloc_plan_info(const ffai_attn_desc* d, int32_t info[5], size_t
   if (rc != FFAI_OK) return fail(rc, why);
   const Plan p = make_plan(d, true, true, kScratchBytes);
   info[0] = p.decode ? 1 : 0;
-  info[1] = p.decode ? p.waves : p.variant;
+  info[1] = p.decode ? p.waves : (p.x16 ? ffai::kWave4x2x16 : p.variant);
   info[2] = p.n_split;
   info[3] = p.tiles_per_split;
   info[4] = p.n_work;
@@ -855,6 +877,12 @@ int ffai_get_decode_tiles_per_wg(void) { return decode_tiles_per_wg(); }
 void ffai_set_decode_tiles_per_wg(int n) {
   if (n >= 0) g_decode_tps.store(n, std::memory_order_relaxed);
 }
+
+void ffai_set_attn_variant(int variant) {
+  g_attn_variant.store(variant >= 0 && variant <= 3 ? variant : -1, std::memory_order_relaxed);
+}
+
+int ffai_get_attn_variant(void) { return attn_variant(); }
 
 void ffai_set_geometry_override(int cus, int xcds) {
   const bool on = cus > 0 && xcds > 0;

@@ -89,7 +89,8 @@ constexpr int kMaxFwdSplits = 64;
 enum Variant : int {
   kWave1 = 0,   // 1 wave x 32 query rows per workgroup (decode, short queries)
   kWave4 = 1,   // 4 waves x 32 rows (128 rows; head_dim 128 and the f32 kernel)
-  kWave4x2 = 2  // 4 waves x 64 rows (256 rows; 16-bit head_dim 64: two column blocks per wave)
+  kWave4x2 = 2,  // 4 waves x 64 rows (256 rows; 16-bit head_dim 64: two column blocks per wave)
+  kWave4x2x16 = 3  // the same shape on 16x16x32 MFMA (fwd16_kernel, attn_kernels16.cuh)
 };
 inline int block_m_of(int variant) { return variant == kWave1 ? 32 : variant == kWave4 ? 128 : 256; }
 

@@ -2,6 +2,7 @@
 #pragma once
 
 #include "attn_kernels.cuh"
+#include "attn_kernels16.cuh"
 
 namespace ffai {
 namespace {
@@ -21,6 +22,14 @@ hipError_t launch_one(const FwdParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int MODE, int OUTT, bool KT>
+hipError_t launch_x16(const FwdParams& p, hipStream_t s) {
+  const int xr = 1 << p.xcd_shift;
+  const unsigned grid = (unsigned)(p.sec1_wgs + (p.n_work - p.sec1_work + xr - 1) / xr * xr);
+  hipLaunchKernelGGL((fwd16_kernel<MODE, OUTT, KT>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 // Launch shapes instantiated per head_dim and dtype (see Variant in attn_kernels.h).
 template <int MODE, int KVT, int OUTT, int D, bool KT>
 hipError_t pick_variant(const FwdParams& p, int variant, hipStream_t s) {
@@ -29,6 +38,9 @@ hipError_t pick_variant(const FwdParams& p, int variant, hipStream_t s) {
     case kWave4: return launch_one<MODE, KVT, OUTT, D, KT, 4, 1>(p, s);
     case kWave4x2:
       if constexpr (MODE != kF32 && D == 64) return launch_one<MODE, KVT, OUTT, D, KT, 4, 2>(p, s);
+      return hipErrorInvalidValue;
+    case kWave4x2x16:
+      if constexpr (MODE != kF32 && D == 64) return launch_x16<MODE, OUTT, KT>(p, s);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }

@@ -128,7 +128,8 @@ size_t ffai_attn_noalloc_scratch_bytes(void);
  * every operand admits the kernels' vector accesses (16-byte aligned bases and strides), so a
  * test or benchmark can state which kernel shape it ran. info[0]: kernel (0 the fused
  * encoder/prefill kernel, 1 the decode kernel); info[1]: workgroup shape (fused: 0 one wave x
- * 32 query rows, 1 four waves x 32 rows, 2 four waves x 64 rows; decode: waves per workgroup);
+ * 32 query rows, 1 four waves x 32 rows, 2 four waves x 64 rows, 3 the same on 16x16x32 MFMA;
+ * decode: waves per workgroup);
  * info[2]: key splits per work item (1 = no partials); info[3]: 64-key tiles per split;
  * info[4]: workgroups. Returns FFAI_OK, FFAI_DECLINED or FFAI_ERR_INVALID as
  * ffai_attn_workspace_bytes. */
@@ -208,6 +209,14 @@ void ffai_set_decode_tiles_per_wg(int n);
  * never its result beyond f32 rounding. */
 void ffai_set_fwd_split_override(int items, int pieces);
 void ffai_get_fwd_split_override(int* items, int* pieces);
+
+/* Tuning and test hook, no counterpart in the reference: force the fused kernel's launch shape
+ * (0 one wave x 32 query rows, 1 four waves x 32, 2 four waves x 64, 3 four waves x 64 on the
+ * 16x16x32-MFMA kernel; the last two for 16-bit head_dim 64 only) or -1 for the planner's choice.
+ * Initialised from FFAI_ATTN_VARIANT on first use. It changes plans, never results beyond f32
+ * rounding. Shape 3 is kept as a measured alternative: it is never chosen by the planner. */
+void ffai_set_attn_variant(int variant);
+int ffai_get_attn_variant(void);
 
 /* Tuning and test hook, no counterpart in the reference: the device geometry the launch plans
  * balance over. By default the current device's CUs and XCDs (hipDeviceAttributeMultiprocessorCount,

@@ -144,6 +144,8 @@ extern "C" {
     pub fn ffai_set_decode_min_keys(n: c_int);
     pub fn ffai_get_decode_tiles_per_wg() -> c_int;
     pub fn ffai_set_decode_tiles_per_wg(n: c_int);
+    pub fn ffai_set_attn_variant(variant: c_int);
+    pub fn ffai_get_attn_variant() -> c_int;
     pub fn ffai_set_geometry_override(cus: c_int, xcds: c_int);
     pub fn ffai_set_fwd_split_override(items: c_int, pieces: c_int);
     pub fn ffai_get_fwd_split_override(items: *mut c_int, pieces: *mut c_int);

@@ -17,8 +17,13 @@ Two precisions: the reference's own (f32 queries; f32 self-attention caches, f16
 cache: text_decoder.rs:771-793, the f32 decode kernel) and this build's device caches (bf16
 queries and caches, the 16-bit decode kernel). Weights and inputs are SYNTHETIC and seeded (real
 Whisper weights are not available here): W ~ N(0, 1/d) in f16, E ~ N(0, 1/d), x ~ N(0, 1), K/V
-~ N(0, 1), cache lengths uniform in [1, 448]. Every token must match; the test reports the
-mismatches and the smallest top-2 logit margin among the positions.
+~ N(0, 1), cache lengths uniform in [1, 448].
+
+Criterion: with eps the largest difference between the two chains' logits, a token can only
+differ where the oracle's top-2 margin is below 2 eps; every token with a larger margin must
+match, and eps must stay below a stated bound (1e-3 for the f32 chain, 6e-2 for the bf16 one:
+the attention's own bars, 1e-4 and 2e-2, carried through an out-projection of unit gain). The f32
+chain must match every token. The test prints the mismatches, eps and the near-ties.
 """
 
 from __future__ import annotations
@@ -66,7 +71,7 @@ def test_decode_step_argmax_on_device_logits(gpu, head, precision):
     rnd = (lambda a: a) if ref else (lambda a: okv.round_to(a, "bf16"))
     rnd_x = (lambda a: a.astype(np.float16).astype(np.float32)) if ref else rnd
     dev = lambda a, t: torch.from_numpy(np.ascontiguousarray(a)).to(gpu, t)
-    mismatches, margins, n = 0, [], 0
+    mismatches, margins, n, eps, guarded = 0, [], 0, 0.0, 0
     for pos in range(POSITIONS):
         rng = np.random.default_rng(900 + pos)
         x = rng.standard_normal((BEAMS, D_MODEL)).astype(np.float32)
@@ -106,12 +111,21 @@ def test_decode_step_argmax_on_device_logits(gpu, head, precision):
         rlog = og.vocab_logits(vq, vsc, vcorr, rh2, 32)
         tok_ref = rlog.argmax(axis=1)
 
-        mismatches += int((tok_gpu != tok_ref).sum())
         top2 = np.sort(rlog, axis=1)[:, -2:]
-        margins.extend((top2[:, 1] - top2[:, 0]).tolist())
+        margin = top2[:, 1] - top2[:, 0]
+        e = float(np.abs(logits.cpu().numpy().astype(np.float64) - rlog).max())
+        eps = max(eps, e)
+        clear = margin > 2 * e  # a token that no logit difference of size e can flip
+        assert (tok_gpu[clear] == tok_ref[clear]).all(), (pos, margin, e)
+        guarded += int(clear.sum())
+        mismatches += int((tok_gpu != tok_ref).sum())
+        margins.extend(margin.tolist())
         n += BEAMS
         if ref:  # f32 attention: the device's residual stream tracks the oracle's closely
             assert np.abs(h2.cpu().numpy() - rh2).max() < 1e-3
-    print(f"argmax chain ({precision}): {n} tokens, {mismatches} mismatches, smallest top-2 "
-          f"margin {min(margins):.4f}")
-    assert mismatches == 0
+    print(f"argmax chain ({precision}): {n} tokens, {mismatches} mismatches, logit difference "
+          f"{eps:.2e}, {n - guarded} tokens within 2x of it (near-ties), smallest top-2 margin "
+          f"{min(margins):.4f}")
+    assert eps < (1e-3 if ref else 6e-2)
+    if ref:
+        assert mismatches == 0

@@ -57,7 +57,10 @@ def _run_encoder(gpu, q, kt, v, dtype, out_dtype, expect_plan):
     plan = fa.plan(qd, kd, vd, out, k_transposed=True, scale=scale)
     print("plan", plan)
     for key, val in expect_plan.items():
-        assert plan[key] == val, (key, plan)
+        if key == "shape" and val == "wave4x2":  # either kernel of the four-wave x 64-row shape
+            assert plan[key] in ("wave4x2", "wave4x2x16"), plan
+        else:
+            assert plan[key] == val, (key, plan)
     assert fa.attention(qd, kd, vd, k_transposed=True, scale=scale, out=out) is not None
     got = out.float().cpu().numpy()
     want = oracle.attend_general(q, kt, v, k_transposed=True, scale=scale, threads=THREADS)

@@ -193,7 +193,7 @@ def test_noalloc_plan_is_the_fwd_plan_capped_to_the_scratch(args):
     fwd = L.plan_info(d)
     fwd_info = (1 if fwd["kernel"] == "decode" else 0,
                 fwd["shape"] if fwd["kernel"] == "decode" else
-                ("wave1", "wave4", "wave4x2").index(fwd["shape"]),
+                ("wave1", "wave4", "wave4x2", "wave4x2x16").index(fwd["shape"]),
                 fwd["splits"], fwd["tiles_per_split"], fwd["workgroups"])
     na = L.noalloc_plan_info(d)
     assert na["bytes"] <= cap
