@@ -19,8 +19,8 @@ bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras] [--eager]
                        [--layers L]
-                       [--legs decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes
-                               | none | copy]
+                       [--legs decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes,
+                               stamps | none | copy]
 """
 
 from __future__ import annotations
@@ -50,10 +50,11 @@ def parse():
                     help="decode leg without HIP graphs (for counter collection)")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--legs",
-                    default="decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes",
+                    default="decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes,"
+                            "stamps",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "decode_ref, state, block, gemv, tiny, small, prefill, floor, pipes, or "
-                         "'none'; "
+                         "decode_ref, state, block, gemv, tiny, small, prefill, floor, pipes, "
+                         "stamps, or 'none'; "
                          "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
@@ -466,6 +467,107 @@ def decode_ref_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, 
         "note": ("bytes count each call's reads as the reference issues them: the cross K/V "
                  "once per beam"),
     }
+
+
+def stamps_bench(torch, fa, calls=3):
+    """Where the kernels' time goes, from the diagnostic library (libffai_attn_stamps.so: the same
+    sources built with FFAI_STAMPS, whose kernels time their phases with s_memtime and write the
+    results with vector stores; the product library has none of it). Two workloads:
+      * the fused kernel on one whisper-large-v3 layer (B16 H20 T1500, bf16, K^T): per wave, the
+        sums over its tiles of phase B (S^T of subtile 1 with subtile 0's exps), the settle check
+        of subtile 0, phase C (PV of subtile 0 with subtile 1's exps), the settle check of
+        subtile 1, the barrier (the DMA wait and the workgroup), and D (staging, PV of subtile 1,
+        S^T of the next tile's subtile 0); shares of the loop and cycles per tile;
+      * the 16-bit decode kernel on the beam-5 whisper-medium step's cross-attention (5 beams as
+        rows, 16 heads x 1500 frames, K as rows: 8 key splits) and self-attention (5 ragged beam
+        caches of <= 448 keys): each workgroup's event times from its entry (first K/V load
+        issued, first tile landed, tiles done, LDS merge done, end), for the workgroups that
+        wrote the output and those that only passed a split partial on.
+    Timing adds ~20% to the fused kernel (the counter reads wait for outstanding LDS reads);
+    the shares, not the absolute times, are what this leg is for. Ticks are converted with the
+    100 MHz real-time counter read beside them."""
+    import ctypes
+    import statistics as stats
+
+    from ffai_amd import build as fbuild
+
+    lib = ctypes.CDLL(fbuild.STAMPS_LIB_PATH)
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    lib.ffai_attn_fwd.argtypes = [ctypes.c_void_p, vp, vp, vp, vp, vp, sz, vp]
+    lib.ffai_attn_fwd.restype = ctypes.c_int
+    lib.ffai_attn_workspace_bytes.argtypes = [ctypes.c_void_p, ctypes.POINTER(sz)]
+    lib.ffai_attn_workspace_bytes.restype = ctypes.c_int
+    lib.ffai_stamps_set.argtypes = [vp, sz]
+    lib.ffai_stamps_set.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+
+    def run(q, k, v, out, rec_bytes, **kw):
+        d = fa.make_desc(q, k, v, out, k_transposed=kw.get("k_transposed", False),
+                         scale=kw.get("scale", 1.0), causal=False, q_offset=0,
+                         kv_lens=kw.get("kv_lens"))
+        n = ctypes.c_size_t(0)
+        assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
+        ws = torch.zeros(max(16, n.value), dtype=torch.uint8, device=dev)
+        buf = torch.zeros(rec_bytes // 8, dtype=torch.int64, device=dev)
+        for i in range(calls):  # the last call records
+            lib.ffai_stamps_set(buf.data_ptr() if i == calls - 1 else None, rec_bytes)
+            rc = lib.ffai_attn_fwd(ctypes.byref(d), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), ws.data_ptr(), ws.numel(), stream.cuda_stream)
+            assert rc == 0, rc
+        torch.cuda.synchronize()
+        lib.ffai_stamps_set(None, 0)
+        return buf.cpu().numpy().astype("uint64")
+
+    g = torch.Generator(device=dev).manual_seed(4)
+    # ---- fused kernel, one whisper-large-v3 layer
+    B, H, T, D = 16, 20, 1500, 64
+    q = torch.randn(B, H, T, D, generator=g, device=dev).bfloat16()
+    kt = torch.randn(B, H, D, T, generator=g, device=dev).bfloat16()
+    v = torch.randn(B, H, T, D, generator=g, device=dev).bfloat16()
+    o = torch.empty_like(q)
+    wgs = 2048
+    r = run(q, kt, v, o, wgs * 1024, k_transposed=True, scale=0.125).reshape(wgs, 4, 32)
+    rec = r[r[:, :, 6].astype("int64") > 0]      # waves that ran tiles
+    names = ["B", "settle0", "C", "settle1", "barrier", "D"]
+    sums = rec[:, :6].astype("float64").sum(axis=0)
+    tiles = float(rec[:, 6].sum())
+    ticks_per_ns = stats.median(((rec[:, 9] - rec[:, 7]) / ((rec[:, 10] - rec[:, 8]) * 10.0)).tolist())
+    enc = {"waves": int(len(rec)), "tiles_per_wave": tiles / len(rec),
+           "share": {n: float(x / sums.sum()) for n, x in zip(names, sums)},
+           "ticks_per_tile": float(sums.sum() / tiles),
+           "ns_per_tile": float(sums.sum() / tiles / ticks_per_ns),
+           "clock_ticks_per_ns": float(ticks_per_ns)}
+    # ---- decode kernel, beam-5 cross- and self-attention of one whisper-medium layer
+    Hd, beams, Te, cap = 16, 5, 1500, 448
+    out = {"encoder_large_v3_layer": enc}
+    qx = torch.randn(1, Hd, beams, D, generator=g, device=dev).bfloat16()
+    kx = torch.randn(1, Hd, Te, D, generator=g, device=dev).bfloat16()
+    vx = torch.randn(1, Hd, Te, D, generator=g, device=dev).bfloat16()
+    ox = torch.empty(1, Hd, beams, D, device=dev)
+    gl = torch.Generator(device="cpu").manual_seed(3)
+    lens = torch.randint(1, cap + 1, (beams,), generator=gl, dtype=torch.int32).to(dev)
+    qs = torch.randn(beams, Hd, 1, D, generator=g, device=dev).bfloat16()
+    ks = torch.randn(beams, Hd, cap, D, generator=g, device=dev).bfloat16()
+    vs = torch.randn(beams, Hd, cap, D, generator=g, device=dev).bfloat16()
+    os_ = torch.empty(beams, Hd, 1, D, device=dev)
+    events = ["issued", "landed", "tiles_done", "lds_merged", "end"]
+    for name, args, kw in (("decode_cross_beam5", (qx, kx, vx, ox), dict(scale=0.125)),
+                           ("decode_self_beam5", (qs, ks, vs, os_),
+                            dict(scale=0.125, kv_lens=lens))):
+        nw = 1024
+        r = run(*args, nw * 64, **kw).reshape(nw, 8)
+        r = r[r[:, 0] > 0]
+        rel = (r[:, 1:6].astype("int64") - r[:, :1].astype("int64")) / ticks_per_ns
+        wrote = r[:, 6] == 1
+        leg = {"workgroups": int(len(r))}
+        for tag, m in (("writers", wrote), ("split_only", ~wrote)):
+            if m.any():
+                leg[tag] = {"count": int(m.sum()),
+                            **{f"{e}_ns": float(stats.median(rel[m, i].tolist()))
+                               for i, e in enumerate(events)}}
+        out[name] = leg
+    return out
 
 
 # ------------------------------------------------------------------------------------------
@@ -1041,6 +1143,15 @@ def main():
         log(f"launch floor: empty {fl['empty_us']:.2f} us, 6 MB read "
             + ", ".join(f"{k} WGs {v:.2f} us" for k, v in fl["read_us"].items()))
         extras["launch_floor"] = fl
+    if "stamps" in legs:
+        log("phase stamps: fused kernel (large-v3 layer) and decode kernel (beam-5 layer) ...")
+        stp = stamps_bench(torch, fa)
+        e = stp["encoder_large_v3_layer"]
+        log("phase stamps: encoder " + ", ".join(f"{k} {v:.1%}" for k, v in e["share"].items())
+            + f"; {e['ns_per_tile']:.0f} ns per tile per wave")
+        for name in ("decode_cross_beam5", "decode_self_beam5"):
+            log(f"phase stamps: {name} {stp[name]}")
+        extras["phase_stamps"] = stp
     if "pipes" in legs:
         log("pipe rates: MFMA, v_exp_f32, FMA and mixes ...")
         pr = pipes_bench(torch)

@@ -95,17 +95,31 @@ def _run(cmd: list[str], verbose: bool) -> dict:
     return _resources(res.stderr)
 
 
+# The diagnostic library: the attention sources compiled with FFAI_STAMPS, so that the fused and
+# decode kernels record their phase times (bench.py --legs stamps). The product library's code
+# is unaffected; nothing but that benchmark leg loads this one.
+STAMPS_LIB_PATH = os.path.join(HERE, "libffai_attn_stamps.so")
+STAMPS_SOURCES = [os.path.join(CSRC, n) for n in
+                  ("fwd_bf16.hip", "fwd_f16.hip", "fwd_f32.hip", "decode.hip", "decode_f16.hip",
+                   "decode_vec.hip", "attn_launch.hip", "attn_api.cpp")]
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every source (always) into objects in parallel, then link LIB_PATH."""
+    """Compile every source (always) into objects in parallel, then link LIB_PATH and the
+    diagnostic STAMPS_LIB_PATH."""
     from concurrent.futures import ThreadPoolExecutor
 
     os.makedirs(BUILD_DIR, exist_ok=True)
     cc = hipcc()
-    objs, cmds = [], []
+    objs, sobjs, cmds = [], [], []
     for src in SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
         objs.append(obj)
         cmds.append([cc] + flags() + [_REMARK, "-c", "-x", "hip", src, "-o", obj])
+    for src in STAMPS_SOURCES:
+        obj = os.path.join(BUILD_DIR, "stamps_" + os.path.basename(src) + ".o")
+        sobjs.append(obj)
+        cmds.append([cc] + flags() + ["-DFFAI_STAMPS", "-c", "-x", "hip", src, "-o", obj])
     jobs = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 8)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         usage = {}
@@ -113,9 +127,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
             usage.update(r)
     with open(RESOURCES_PATH, "w") as f:
         json.dump(usage, f, indent=0, sort_keys=True)
-    tmp = LIB_PATH + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + LIBS, verbose)
-    os.replace(tmp, LIB_PATH)
+    for path, os_ in ((LIB_PATH, objs), (STAMPS_LIB_PATH, sobjs)):
+        tmp = path + ".tmp"
+        _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + os_ + LIBS, verbose)
+        os.replace(tmp, path)
     return LIB_PATH
 
 

@@ -512,6 +512,13 @@ int scratch_for_current(void** ptr) {
   return FFAI_OK;
 }
 
+#ifdef FFAI_STAMPS
+// Diagnostic library only (libffai_attn_stamps.so, built with FFAI_STAMPS): the device buffer
+// the kernels write their phase times into (see attn_common.cuh), set by ffai_stamps_set.
+std::atomic<uint64_t*> g_stamp_buf{nullptr};
+std::atomic<size_t> g_stamp_bytes{0};
+#endif
+
 // `use_scratch`: the partials go to the library's scratch (ws and ws_bytes are ignored).
 int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v, void* out,
             void* ws, size_t ws_bytes, void* stream, bool allow_split, bool use_scratch = false) {
@@ -577,6 +584,10 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
     p.causal = d->causal; p.q_offset = d->q_offset;
     p.n_split = pl.n_split; p.tiles_per_split = pl.tiles_per_split; p.n_work = pl.n_work;
     p.scale_log2 = d->scale * 1.4426950408889634f;
+#ifdef FFAI_STAMPS
+    p.stamps = g_stamp_buf.load();
+    p.stamp_wgs = (int)std::min<size_t>(g_stamp_bytes.load() / 64, INT32_MAX);
+#endif
     const hipError_t e = f32 ? ffai::launch_decode_vec(p, kvt, kt, pl.waves, s)
                              : ffai::launch_decode(p, mode, ot, d->head_dim, kt, pl.waves, s);
     if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("decode launch: ") + hipGetErrorString(e));
@@ -614,6 +625,10 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
             int64_t(ffai::kBlockN) * d->v_strides[2] * 2 < lim;
   }
   p.scale_log2 = d->scale * 1.4426950408889634f;
+#ifdef FFAI_STAMPS
+  p.stamps = g_stamp_buf.load();
+  p.stamp_wgs = (int)std::min<size_t>(g_stamp_bytes.load() / 1024, INT32_MAX);
+#endif
   const hipError_t e = ffai::launch_fwd(p, mode, kvt, ot, d->head_dim, kt,
                                         pl.x16 ? ffai::kWave4x2x16 : pl.variant, s);
   if (e != hipSuccess) return fail(FFAI_ERR_HIP, std::string("fwd launch: ") + hipGetErrorString(e));
@@ -905,6 +920,17 @@ void ffai_set_decode_min_keys(int n) {
 }
 
 const char* ffai_attn_last_error(void) { return g_last_error.c_str(); }
+
+#ifdef FFAI_STAMPS
+// Diagnostic library only: record phase times of the fused kernel's 16-bit path (1024 bytes per
+// workgroup: 4 waves x 32 u64) and the 16-bit decode kernel (64 bytes per workgroup) into
+// `buf` (device memory, `bytes` long; workgroups past it record nothing). NULL stops recording.
+int ffai_stamps_set(void* buf, size_t bytes) {
+  g_stamp_bytes.store(buf ? bytes : 0);
+  g_stamp_buf.store(static_cast<uint64_t*>(buf));
+  return FFAI_OK;
+}
+#endif
 
 int ffai_attn_abi_version(void) { return FFAI_ATTN_ABI_VERSION; }
 

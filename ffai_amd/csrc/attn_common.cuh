@@ -174,6 +174,44 @@ __device__ __forceinline__ int wg_id_y() { return (int)__builtin_amdgcn_workgrou
 __device__ __forceinline__ int wg_id_z() { return (int)__builtin_amdgcn_workgroup_id_z(); }
 __device__ __forceinline__ int item_id() { return (int)__builtin_amdgcn_workitem_id_x(); }
 
+#ifdef FFAI_STAMPS
+// ---------------------------------------------------------------------------------------------
+// Phase timestamps, compiled only into the diagnostic library (FFAI_STAMPS,
+// libffai_attn_stamps.so; the product library's code has none of this). Times come from the
+// shader clock counter (s_memtime) and, for calibration, the 100 MHz real-time counter
+// (s_memrealtime); both are scalar reads. Results are written from one lane with vector buffer
+// stores.
+// Layout of the fused kernel's record (16-bit path), per recording workgroup and wave, 32 u64:
+//   [0..5] phase sums over the wave's tiles, in s_memtime ticks: B, settle 0, C, settle 1,
+//          barrier (the wait for the tile's DMA and the workgroup), D (staging and the last
+//          products); [6] tiles; [7] s_memtime and [8] s_memrealtime at the loop's start, [9]
+//          and [10] at its end; [11] s_memrealtime at kernel entry, [12] after the wave's last
+//          store was issued and [13] once its stores were acknowledged; [14] where the wave ran:
+//          HW_ID (wave slot, SIMD, CU, shader array, engine) in the low 32 bits, the XCC in the
+//          high; [15] s_memrealtime once the prologue's Q loads and first tile copies were
+//          issued, [16] once they landed and [17] after the workgroup barrier that follows;
+//          [18..31] zero.
+// The decode kernel's record, per recording workgroup (wave 0), 8 u64 of s_memtime: [0] entry,
+// [1] first K/V load issued, [2] first tile landed, [3] tile loop done, [4] waves' partials
+// merged in LDS, [5] end; [6] 1 if this workgroup wrote the output (unsplit, or the unit's last
+// split), [7] s_memrealtime at entry.
+__device__ __forceinline__ uint64_t stamp_clock() { return __builtin_amdgcn_s_memtime(); }
+__device__ __forceinline__ uint64_t stamp_realtime() { return __builtin_amdgcn_s_memrealtime(); }
+// HW_ID (hardware register 4) and XCC_ID (register 20), read whole: s_getreg's operand is
+// register | offset << 6 | (bits - 1) << 11.
+__device__ __forceinline__ uint64_t stamp_where() {
+  const uint32_t hw = __builtin_amdgcn_s_getreg(4 | (31 << 11));
+  const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (15 << 11));
+  return ((uint64_t)xcc << 32) | hw;
+}
+__device__ __forceinline__ void stamp_put(uint64_t* base, int64_t index, uint64_t value) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(base, (short)0, 0x7fffffff, kBufferWord3);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, value), r, (int)(index * 8), 0,
+                                        0);
+}
+#endif
+
 template <int DT>
 __device__ __forceinline__ f32x16 mfma16(u32x4 a, u32x4 b, f32x16 c) {
   if constexpr (DT == kBF16) {

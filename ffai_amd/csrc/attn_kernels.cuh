@@ -82,6 +82,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
 
   // ---- which work (an item, or one piece of a split item) this workgroup computes
   const int hw = blockIdx.x;
+#ifdef FFAI_STAMPS
+  const uint64_t st_e0 = stamp_realtime();
+  uint64_t st_pro[3] = {0, 0, 0};  // prologue: loads issued, loads landed, barrier passed
+#define FFAI_STAMP_PRO(i) \
+  __builtin_amdgcn_sched_barrier(0); \
+  st_pro[i] = stamp_realtime(); \
+  __builtin_amdgcn_sched_barrier(0)
+#else
+#define FFAI_STAMP_PRO(i)
+#endif
   int work;
   const int xs = p.xcd_shift, xm = (1 << xs) - 1;  // XCDs: 1 << xs
   if (hw < p.sec1_wgs) {
@@ -427,10 +437,14 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     } else {
       stage_tile(0, 0, t_begin);
       if (t_begin + 1 < t_end) stage_tile(1, 1, t_begin + 1);
+      FFAI_STAMP_PRO(0);
       vm_wait_all();
+      FFAI_STAMP_PRO(1);
     }
   }
   __syncthreads();
+  FFAI_STAMP_PRO(2);
+#undef FFAI_STAMP_PRO
 
   // Mask the keys of 32-key subtile `st` past each row's end (ragged tail, causal diagonal).
   // sacc[c][st][i] <-> key kb + 32st + 8(i/4) + 4g + i%4 of query q0 + 32c + n32.
@@ -823,27 +837,44 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
         for (int c = 0; c < QW; ++c) m_s[c] = 0.f;
       }
     }
+#ifdef FFAI_STAMPS
+    // phase times of this wave (diagnostic builds only; see attn_common.cuh)
+    uint64_t st_acc[6] = {0, 0, 0, 0, 0, 0};
+    uint64_t st_tiles = 0;
+    const uint64_t st_c0 = stamp_clock(), st_r0 = stamp_realtime();
+#define FFAI_STAMP_AT(var) \
+  __builtin_amdgcn_sched_barrier(0); \
+  const uint64_t var = stamp_clock(); \
+  __builtin_amdgcn_sched_barrier(0)
+#else
+#define FFAI_STAMP_AT(var)
+#endif
     for (int it = t_begin; it < t_end; ++it) {
       const LT* kl = k_lds + ((it - t_begin) % NBK) * KBUF;
       const LT* vl = v_lds + ((it - t_begin) % NBUF) * VBUF;
       const int kb = it * BN;
       const bool need_mask = need_mask_of(it);
+      FFAI_STAMP_AT(st_t0);
       zero_sub(1);
       // B
       __builtin_amdgcn_sched_barrier(0);
       if (D == 64 && fast) phase_b(kl, kFastTag);
       else phase_b(kl, kSlowTag);
       __builtin_amdgcn_sched_barrier(0);
+      FFAI_STAMP_AT(st_t1);
       settle(0);
       rescale();
       if (need_mask) mask_subtile(sacc, kb, 1);
+      FFAI_STAMP_AT(st_t2);
       // C
       __builtin_amdgcn_sched_barrier(0);
       if (D == 64 && fast) phase_c(vl, kFastTag);
       else phase_c(vl, kSlowTag);
       __builtin_amdgcn_sched_barrier(0);
+      FFAI_STAMP_AT(st_t3);
       settle(1);
       rescale();
+      FFAI_STAMP_AT(st_t4);
       // Publish tile it + 1 (staged one iteration ago; the barrier also awaits its DMA), then
       // stage tile it + 2 into the buffer of tile it - 1, which every wave has finished with
       // once it passes this barrier.
@@ -851,6 +882,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
       const int nkbuf = (it + 1 - t_begin) % NBK;
       vm_wait_all();
       __syncthreads();
+      FFAI_STAMP_AT(st_t5);
       if (it + 2 < t_end) stage_tile((it + 2 - t_begin) % NBK, (it + 2 - t_begin) % NBUF, it + 2);
       // D: O^T += V^T P^T for subtile 1, and S^T of the next tile's subtile 0
       pv(vl, 1);
@@ -859,9 +891,50 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
         qk(sacc, k_lds + nkbuf * KBUF, 0);
         if (need_mask_of(it + 1)) mask_subtile(sacc, (it + 1) * BN, 0);
       }
+#ifdef FFAI_STAMPS
+      FFAI_STAMP_AT(st_t6);
+      st_acc[0] += st_t1 - st_t0;
+      st_acc[1] += st_t2 - st_t1;
+      st_acc[2] += st_t3 - st_t2;
+      st_acc[3] += st_t4 - st_t3;
+      st_acc[4] += st_t5 - st_t4;
+      st_acc[5] += st_t6 - st_t5;
+      ++st_tiles;
+#endif
     }
+#ifdef FFAI_STAMPS
+#undef FFAI_STAMP_AT
+    if (p.stamps && hw < p.stamp_wgs && lane == 0) {
+      const uint64_t st_c1 = stamp_clock(), st_r1 = stamp_realtime();
+      const int64_t rec = ((int64_t)hw * NW + wave) * 32;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) stamp_put(p.stamps, rec + k, st_acc[k]);
+      stamp_put(p.stamps, rec + 6, st_tiles);
+      stamp_put(p.stamps, rec + 7, st_c0);
+      stamp_put(p.stamps, rec + 8, st_r0);
+      stamp_put(p.stamps, rec + 9, st_c1);
+      stamp_put(p.stamps, rec + 10, st_r1);
+    }
+#endif
   }
 
+#ifdef FFAI_STAMPS
+  // entry and exit times and the wave's hardware slot (recording workgroups, lane 0)
+  auto stamp_exit = [&]() {
+    if (p.stamps && hw < p.stamp_wgs && lane == 0) {
+      const uint64_t e1 = stamp_realtime();
+      vm_wait_all();
+      const uint64_t e2 = stamp_realtime();
+      const int64_t rec = ((int64_t)hw * NW + wave) * 32;
+      stamp_put(p.stamps, rec + 11, st_e0);
+      stamp_put(p.stamps, rec + 12, e1);
+      stamp_put(p.stamps, rec + 13, e2);
+      stamp_put(p.stamps, rec + 14, stamp_where());
+#pragma unroll
+      for (int k = 0; k < 3; ++k) stamp_put(p.stamps, rec + 15 + k, st_pro[k]);
+    }
+  };
+#endif
   // ---- epilogue: oacc[c][dt][4r + e] <-> d = 32dt + 8r + 4g + e of query q0 + 32c + n32
   float l_tot[QW];
 #pragma unroll
@@ -925,7 +998,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
       *s_last = (done == S - 1) ? 1 : 0;
     }
     __syncthreads();
-    if (!*s_last) return;
+    if (!*s_last) {
+#ifdef FFAI_STAMPS
+      stamp_exit();
+#endif
+      return;
+    }
     // Merge all S pieces (this one's too, as stored) in piece order, so that the result does not
     // depend on which piece finished last: KP pieces' loads in flight per round trip.
     constexpr int KP = 2;
@@ -1001,6 +1079,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
         else st4<OUTT, false>(op + 32 * dt + 8 * r + 4 * g, x);
       }
   }
+#ifdef FFAI_STAMPS
+  stamp_exit();
+#endif
 }
 
 }  // namespace

@@ -47,6 +47,10 @@ struct FwdParams {
   int32_t dma;               // 16-bit: whole tiles may go global -> LDS by DMA (aligned, and
                              // each lane's byte offset within a K or V tile fits 32 bits)
   float scale_log2;          // scale * log2(e)
+#ifdef FFAI_STAMPS
+  uint64_t* stamps;          // diagnostic builds only: per-wave phase times (attn_common.cuh)
+  int32_t stamp_wgs;         // workgroups (by hardware index) that record them
+#endif
 };
 
 // A decode launch: at most 32 query rows (group x Tq) per (batch, kv-head) unit, operands that
@@ -69,6 +73,10 @@ struct DecodeParams {
   int32_t tiles_per_split;  // 64-key tiles per workgroup
   int32_t n_work;           // B * Hkv * n_split
   float scale_log2;
+#ifdef FFAI_STAMPS
+  uint64_t* stamps;         // diagnostic builds only: per-workgroup event times
+  int32_t stamp_wgs;        // workgroups (by linear hardware index) that record them
+#endif
 };
 // Workspace layout shared by every plan: kCounterBytes of split counters (decode units or split
 // fwd items, one int32 each; zero at rest) first, then the partials of whichever kernel the plan

@@ -43,8 +43,9 @@ __device__ __forceinline__ void store_row_chunk(const DecodeParams& p, int b, in
 // n * OROW, then the rows' maxima (scaled log2 units) at MR * OROW + n and weight sums at
 // MR * OROW + MR + n. Every thread of the workgroup calls it, after a barrier that publishes the
 // partials.
+// Returns true when this workgroup wrote the unit's rows (unsplit, or the unit's last split).
 template <int OUTT, int D, int NWD, int OROW, int MR, int WST>
-__device__ __forceinline__ void finish_unit(const DecodeParams& p, const float* mbase, int b,
+__device__ __forceinline__ bool finish_unit(const DecodeParams& p, const float* mbase, int b,
                                             int hk, int unit, int split, int R, int tid) {
   constexpr int C4 = D / 4;  // 4-float chunks per row
   const int items = R * C4;
@@ -91,7 +92,7 @@ __device__ __forceinline__ void finish_unit(const DecodeParams& p, const float* 
                                               kDeviceScope);
     }
   }
-  if (p.n_split == 1) return;
+  if (p.n_split == 1) return true;
 
   // ---- count this split; the unit's last one merges them all.
   // Ordering: every thread waits for its partial stores to be acknowledged (vmcnt(0): device-
@@ -111,7 +112,7 @@ __device__ __forceinline__ void finish_unit(const DecodeParams& p, const float* 
     s_last = (done == p.n_split - 1) ? 1 : 0;
   }
   __syncthreads();
-  if (!s_last) return;
+  if (!s_last) return false;
   const int S = p.n_split;
   const int64_t uo = (int64_t)unit * S * R * D;               // the unit's first O row (floats)
   const int64_t uml = o_floats + (int64_t)unit * S * R * 2;   // and its first (m, l) pair
@@ -152,6 +153,7 @@ __device__ __forceinline__ void finish_unit(const DecodeParams& p, const float* 
     store_row_chunk<OUTT, D>(p, b, hk, n, c4, acc, L);
   }
   if (tid == 0) __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
 }
 
 // NC: 16-column blocks of query rows (1 for units of at most 16 rows, 2 for up to 32).
@@ -421,11 +423,22 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     else stage_tile(it);
     if (patch_end_of(kb)) patch_kt_load();
   };
+#ifdef FFAI_STAMPS
+  // event times of the workgroup, recorded by wave 0 (diagnostic builds only; attn_common.cuh)
+  const int st_wg = split + p.n_split * (hk + p.Hkv * b);  // the linear workgroup index
+  const bool st_rec = p.stamps && st_wg < p.stamp_wgs && tid == 0;
+  uint64_t st_e[6];
+  const uint64_t st_r0 = stamp_realtime();
+  st_e[0] = stamp_clock();
+#endif
   // The wave's first tile goes out before the Q loads: the DMA is a compiler barrier for memory
   // accesses, so nothing is outstanding when it is issued. (Issued after them, the compiler made
   // the DMA wait for the Q loads: registers it reuses were load targets on the register-staging
   // path, and one in-order counter covers both.)
   if (iters > 0 && t_begin + wave < t_end) issue_tile(t_begin + wave);
+#ifdef FFAI_STAMPS
+  st_e[1] = stamp_clock();
+#endif
   // ---- Q fragments (issued after the wave's first K/V loads): B operand of S^T, block c,
   //      contraction chunk h: d = 32 h + 8 q4 .. +7 of column 16 c + n16's row
   u32x4 qf[NC][D / 32];
@@ -451,6 +464,9 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     const bool tail_dma = tail_dma_of(kb), end_dma = end_dma_of(kb);
     const bool patch_end = patch_end_of(kb);
     vm_wait_all();
+#ifdef FFAI_STAMPS
+    if (i == 0) st_e[2] = stamp_clock();
+#endif
     if (patch_end) patch_kt_store(it);
     if (tail_dma || end_dma) {
       constexpr int RU = D / 8;  // 16-byte units per V row; the swizzle stays within a row
@@ -555,6 +571,10 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   }
 
   // ---- merge the waves' partials through LDS (the tile area is free once all waves pass here)
+#ifdef FFAI_STAMPS
+  if (iters == 0) st_e[2] = stamp_clock();
+  st_e[3] = stamp_clock();
+#endif
   __syncthreads();
   float* mbase = reinterpret_cast<float*>(lds);
   {
@@ -576,8 +596,20 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     }
   }
   __syncthreads();
-
+#ifdef FFAI_STAMPS
+  st_e[4] = stamp_clock();
+  const bool st_wrote =
+#endif
   finish_unit<OUTT, D, NWD, OROW, 32, WBUF / 2>(p, mbase, b, hk, unit, split, R, tid);
+#ifdef FFAI_STAMPS
+  st_e[5] = stamp_clock();
+  if (st_rec) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) stamp_put(p.stamps, (int64_t)st_wg * 8 + k, st_e[k]);
+    stamp_put(p.stamps, (int64_t)st_wg * 8 + 6, st_wrote ? 1u : 0u);
+    stamp_put(p.stamps, (int64_t)st_wg * 8 + 7, st_r0);
+  }
+#endif
 }
 
 

@@ -71,3 +71,16 @@ def test_no_scalar_register_spills(usage):
     d128_kt = {k: n for k, n in dec.items() if "ELi128ELb1E" in k}
     assert dec.keys() == d128_kt.keys(), sorted(set(dec) - set(d128_kt))
     assert all(n <= 8 for n in d128_kt.values()), d128_kt
+
+
+def test_phase_stamps_only_in_the_diagnostic_library():
+    """The phase-timing instrumentation is compiled only into libffai_attn_stamps.so (bench.py
+    --legs stamps); the product library has none of it."""
+    import ctypes
+
+    from ffai_amd import _lib
+
+    if not os.path.exists(native_build.STAMPS_LIB_PATH):
+        pytest.skip("the diagnostic library has not been built here")
+    assert not hasattr(_lib.load(), "ffai_stamps_set")
+    assert hasattr(ctypes.CDLL(native_build.STAMPS_LIB_PATH), "ffai_stamps_set")
