@@ -20,7 +20,7 @@ bounded sample.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--skip-extras] [--eager]
                        [--layers L]
                        [--legs decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes,
-                               stamps | none | copy]
+                               stamps,keys | none | copy]
 """
 
 from __future__ import annotations
@@ -51,10 +51,10 @@ def parse():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--legs",
                     default="decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes,"
-                            "stamps",
+                            "stamps,keys",
                     help="comma list of extra legs beside the headline encoder run: decode, "
                          "decode_ref, state, block, gemv, tiny, small, prefill, floor, pipes, "
-                         "stamps, or 'none'; "
+                         "stamps, keys, or 'none'; "
                          "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
@@ -469,6 +469,102 @@ def decode_ref_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, 
     }
 
 
+def key_sweep_bench(torch, fa, sets=4, reps=20, key_lens=(1500, 3000, 4500, 6000)):
+    """Fixed and per-key cost of the fused kernel on the large-v3 layer's items: 1920 items of
+    B16 H20, 1500 query rows, bf16, K^T, with 1500 .. 6000 keys (the same items and launch
+    shape; only the key loop grows). A least-squares line through the times gives the per-key
+    rate the loops sustain and the time a launch spends outside them (prologues, epilogues,
+    the tail of the last round)."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    B, H, T, D = 16, 20, 1500, 64
+    pts = []
+    for tk in key_lens:
+        bufs = []
+        for _ in range(sets):
+            q = torch.randn(B, H, T, D, generator=g, device=dev).bfloat16()
+            kt = torch.randn(B, H, D, tk, generator=g, device=dev).bfloat16()
+            v = torch.randn(B, H, tk, D, generator=g, device=dev).bfloat16()
+            bufs.append((q, kt, v, torch.empty_like(q)))
+        nb = fa.workspace_bytes(*bufs[0], k_transposed=True, scale=0.125)
+        ws = torch.zeros(max(nb, 16), dtype=torch.uint8, device=dev) if nb else None
+
+        def once():
+            for q, kt, v, o in bufs:
+                fa.attention(q, kt, v, k_transposed=True, scale=0.125, out=o, workspace=ws)
+
+        for _ in range(3):
+            once()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            once()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * sets)
+        pts.append((tk, us, 4.0 * B * H * T * tk * D / us / 1e6))
+        del bufs, ws
+        torch.cuda.empty_cache()
+    x = np.array([p_[0] for p_ in pts], float)
+    y = np.array([p_[1] for p_ in pts], float)
+    slope, icpt = np.polyfit(x, y, 1)
+    return {"points": [{"keys": k, "us": u, "tflops": f} for k, u, f in pts],
+            "us_per_1500_keys": float(slope * 1500), "fixed_us": float(icpt),
+            "loop_tflops": float(4.0 * B * H * T * 1500 * D / (slope * 1500) / 1e6),
+            "fixed_share_at_1500": float(icpt / (icpt + slope * 1500))}
+
+
+def workgroup_timeline(r):
+    """Per-workgroup times of the fused kernel's record (stamps leg): medians in ns of the
+    prologue (entry -> key loop; of it: entry -> Q loads issued, Q and tiles 0/1 issued -> landed,
+    the barrier and the first product), the key loop, the epilogue (loop end -> last store
+    issued -> acknowledged), the gap from a workgroup's exit to the next workgroup's entry on the
+    same CU (the hardware slot each wave recorded), and the loops' share of the slot-time
+    (2 workgroups per CU x the span from the first entry to the last exit)."""
+    import numpy as np
+
+    a = r.astype("int64")
+    ran = a[:, 0, 6] > 0
+    a = a[ran]
+    base = a[:, :, 11].min()
+    t = lambda k, f: (f(a[:, :, k], axis=1) - base) * 10  # 100 MHz real-time ticks -> ns
+    e0, pre_q, issued, landed = t(11, np.min), t(18, np.max), t(15, np.max), t(16, np.max)
+    bar, l0, l1 = t(17, np.max), t(8, np.min), t(10, np.max)
+    wrote = a[:, 0, 12] > 0
+    x1, x2 = t(12, np.max), t(13, np.max)
+    med = lambda x: float(np.median(x)) if len(x) else None
+    where = a[:, 0, 14]
+    hwid, xcc = where & 0xffffffff, where >> 32
+    cu = xcc * 1000 + ((hwid >> 13) & 7) * 100 + ((hwid >> 12) & 1) * 16 + ((hwid >> 8) & 15)
+    end = np.where(wrote, x2, l1)
+    gaps = []
+    for c in np.unique(cu):
+        idx = np.where(cu == c)[0]
+        idx = idx[np.argsort(e0[idx])]
+        free = []
+        for i in idx:
+            if len(free) < 2:
+                free.append(end[i])
+                continue
+            free.sort()
+            gaps.append(e0[i] - free.pop(0))
+            free.append(end[i])
+    span = float(end.max())
+    return {"workgroups": int(ran.sum()), "cus": int(len(np.unique(cu))),
+            "prologue_ns": med(l0 - e0), "entry_to_q_issue_ns": med(pre_q - e0),
+            "q_and_tiles_issue_ns": med(issued - pre_q), "loads_land_ns": med(landed - issued),
+            "barrier_ns": med(bar - landed), "first_product_ns": med(l0 - bar),
+            "loop_ns_24_tiles": med((l1 - l0)[a[:, 0, 6] == 24]),
+            "epilogue_issue_ns": med((x1 - l1)[wrote]), "store_ack_ns": med((x2 - x1)[wrote]),
+            "exit_to_next_entry_ns": med(np.array(gaps)) if gaps else None,
+            "span_ns": span,
+            "loop_share_of_slot_time": float((l1 - l0).sum() / (2 * len(np.unique(cu)) * span))}
+
+
 def stamps_bench(torch, fa, calls=3):
     """Where the kernels' time goes, from the diagnostic library (libffai_attn_stamps.so: the same
     sources built with FFAI_STAMPS, whose kernels time their phases with s_memtime and write the
@@ -538,6 +634,7 @@ def stamps_bench(torch, fa, calls=3):
            "ticks_per_tile": float(sums.sum() / tiles),
            "ns_per_tile": float(sums.sum() / tiles / ticks_per_ns),
            "clock_ticks_per_ns": float(ticks_per_ns)}
+    enc.update(workgroup_timeline(r))
     # ---- decode kernel, beam-5 cross- and self-attention of one whisper-medium layer
     Hd, beams, Te, cap = 16, 5, 1500, 448
     out = {"encoder_large_v3_layer": enc}
@@ -1143,12 +1240,25 @@ def main():
         log(f"launch floor: empty {fl['empty_us']:.2f} us, 6 MB read "
             + ", ".join(f"{k} WGs {v:.2f} us" for k, v in fl["read_us"].items()))
         extras["launch_floor"] = fl
+    if "keys" in legs:
+        log("key sweep: the large-v3 layer's 1920 items over 1500 .. 6000 keys ...")
+        ks = key_sweep_bench(torch, fa)
+        log("key sweep: " + ", ".join(f"{p_['keys']} keys {p_['us']:.1f} us" for p_ in ks["points"])
+            + f"; per 1500 keys {ks['us_per_1500_keys']:.1f} us ({ks['loop_tflops']:.0f} TFLOP/s"
+            f" in the loops), fixed {ks['fixed_us']:.1f} us ({ks['fixed_share_at_1500']:.1%} of "
+            "the 1500-key launch)")
+        extras["key_sweep_large_v3_items"] = ks
     if "stamps" in legs:
         log("phase stamps: fused kernel (large-v3 layer) and decode kernel (beam-5 layer) ...")
         stp = stamps_bench(torch, fa)
         e = stp["encoder_large_v3_layer"]
         log("phase stamps: encoder " + ", ".join(f"{k} {v:.1%}" for k, v in e["share"].items())
             + f"; {e['ns_per_tile']:.0f} ns per tile per wave")
+        log("phase stamps: encoder workgroups (median ns): prologue "
+            f"{e['prologue_ns']:.0f}, loop of 24 tiles {e['loop_ns_24_tiles']:.0f}, epilogue "
+            f"{e['epilogue_issue_ns']:.0f} + ack {e['store_ack_ns']:.0f}, exit to next entry "
+            f"{e['exit_to_next_entry_ns']:.0f}; loops fill {e['loop_share_of_slot_time']:.1%} "
+            "of the slot-time")
         for name in ("decode_cross_beam5", "decode_self_beam5"):
             log(f"phase stamps: {name} {stp[name]}")
         extras["phase_stamps"] = stp

@@ -186,11 +186,12 @@ __device__ __forceinline__ int item_id() { return (int)__builtin_amdgcn_workitem
 //          barrier (the wait for the tile's DMA and the workgroup), D (staging and the last
 //          products); [6] tiles; [7] s_memtime and [8] s_memrealtime at the loop's start, [9]
 //          and [10] at its end; [11] s_memrealtime at kernel entry, [12] after the wave's last
-//          store was issued and [13] once its stores were acknowledged; [14] where the wave ran:
+//          store was issued and [13] once its stores were acknowledged (zero for a split piece
+//          that leaves the merge to another); [14] where the wave ran:
 //          HW_ID (wave slot, SIMD, CU, shader array, engine) in the low 32 bits, the XCC in the
 //          high; [15] s_memrealtime once the prologue's Q loads and first tile copies were
 //          issued, [16] once they landed and [17] after the workgroup barrier that follows;
-//          [18..31] zero.
+//          [18] before the Q loads are issued; [19..31] zero.
 // The decode kernel's record, per recording workgroup (wave 0), 8 u64 of s_memtime: [0] entry,
 // [1] first K/V load issued, [2] first tile landed, [3] tile loop done, [4] waves' partials
 // merged in LDS, [5] end; [6] 1 if this workgroup wrote the output (unsplit, or the unit's last

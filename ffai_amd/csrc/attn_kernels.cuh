@@ -81,16 +81,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   __shared__ __attribute__((aligned(16))) LT v_lds[NBUF * VBUF];
 
   // ---- which work (an item, or one piece of a split item) this workgroup computes
-  const int hw = blockIdx.x;
+  const int hw = wg_id_x();
 #ifdef FFAI_STAMPS
   const uint64_t st_e0 = stamp_realtime();
-  uint64_t st_pro[3] = {0, 0, 0};  // prologue: loads issued, loads landed, barrier passed
-#define FFAI_STAMP_PRO(i) \
+  // prologue times go to the record as they are taken (nothing stays live across the loop)
+#define FFAI_STAMP_PRO(k) \
   __builtin_amdgcn_sched_barrier(0); \
-  st_pro[i] = stamp_realtime(); \
+  stamp_now(k, stamp_realtime()); \
   __builtin_amdgcn_sched_barrier(0)
 #else
-#define FFAI_STAMP_PRO(i)
+#define FFAI_STAMP_PRO(k)
 #endif
   int work;
   const int xs = p.xcd_shift, xm = (1 << xs) - 1;  // XCDs: 1 << xs
@@ -98,7 +98,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     work = p.xcd_remap ? (hw & xm) * (p.sec1_wgs >> xs) + (hw >> xs) : hw;
     if (work >= p.sec1_work) return;
   } else {
-    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;  // n: a multiple of 1 << xs
+    // n: a multiple of 1 << xs. (gridDim is an out-of-line call, run only by this section's
+    // workgroups; computing n from the parameters instead, with no call left in the kernel,
+    // changes the register allocation of the 16-bit head_dim-64 instantiations to one that
+    // spills.)
+    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;
     work = p.sec1_work + (p.xcd_remap ? (x & xm) * (n >> xs) + (x >> xs) : x);
     if (work >= p.n_work) return;
   }
@@ -125,13 +129,21 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   const int b = bh / p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
 
-  const int tid = threadIdx.x;
+  const int tid = item_id();
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps q0 scalar
   const int g = lane >> 5;    // lane group: which half of each MFMA contraction step
   const int n32 = lane & 31;  // query column of the accumulators
   constexpr int BM = NW * 32 * QW;
   const int q0 = qb * BM + wave * 32 * QW;  // this wave's first query row
+#ifdef FFAI_STAMPS
+  const int64_t st_rec = (p.stamps && hw < p.stamp_wgs) ? ((int64_t)hw * NW + wave) * 32 : -1;
+  auto stamp_now = [&](int k, uint64_t v) {
+    if (st_rec >= 0 && lane == 0) stamp_put(p.stamps, st_rec + k, v);
+  };
+  stamp_now(11, st_e0);
+  stamp_now(14, stamp_where());
+#endif
 
   int kv_end = p.Tk;
   if (p.kv_lens) kv_end = min(kv_end, max(0, p.kv_lens[b]));
@@ -150,6 +162,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   const char* kp_dma = uniform_ptr(reinterpret_cast<const char*>(kp));
   const char* vp_dma = uniform_ptr(reinterpret_cast<const char*>(vp));
 
+  FFAI_STAMP_PRO(18);
   // ---- Q fragments (B operand of S^T = K Q^T), resident for the whole key loop
   constexpr int QF = F32 ? D / 2 : D / 16;
   std::conditional_t<F32, float, u32x4> qf[QW][QF];
@@ -437,13 +450,13 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     } else {
       stage_tile(0, 0, t_begin);
       if (t_begin + 1 < t_end) stage_tile(1, 1, t_begin + 1);
-      FFAI_STAMP_PRO(0);
+      FFAI_STAMP_PRO(15);
       vm_wait_all();
-      FFAI_STAMP_PRO(1);
+      FFAI_STAMP_PRO(16);
     }
   }
   __syncthreads();
-  FFAI_STAMP_PRO(2);
+  FFAI_STAMP_PRO(17);
 #undef FFAI_STAMP_PRO
 
   // Mask the keys of 32-key subtile `st` past each row's end (ragged tail, causal diagonal).
@@ -839,12 +852,15 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     }
 #ifdef FFAI_STAMPS
     // phase times of this wave (diagnostic builds only; see attn_common.cuh)
-    uint64_t st_acc[6] = {0, 0, 0, 0, 0, 0};
-    uint64_t st_tiles = 0;
-    const uint64_t st_c0 = stamp_clock(), st_r0 = stamp_realtime();
+    // (32-bit sums of the low halves of the counter: differences modulo 2^32 are exact for any
+    // phase shorter than 2^32 ticks; fewer scalar registers than 64-bit ones)
+    uint32_t st_acc[6] = {0, 0, 0, 0, 0, 0};
+    uint32_t st_tiles = 0;
+    stamp_now(7, stamp_clock());
+    stamp_now(8, stamp_realtime());
 #define FFAI_STAMP_AT(var) \
   __builtin_amdgcn_sched_barrier(0); \
-  const uint64_t var = stamp_clock(); \
+  const uint32_t var = (uint32_t)stamp_clock(); \
   __builtin_amdgcn_sched_barrier(0)
 #else
 #define FFAI_STAMP_AT(var)
@@ -904,14 +920,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     }
 #ifdef FFAI_STAMPS
 #undef FFAI_STAMP_AT
-    if (p.stamps && hw < p.stamp_wgs && lane == 0) {
+    if (st_rec >= 0 && lane == 0) {
       const uint64_t st_c1 = stamp_clock(), st_r1 = stamp_realtime();
-      const int64_t rec = ((int64_t)hw * NW + wave) * 32;
+      const int64_t rec = st_rec;
 #pragma unroll
       for (int k = 0; k < 6; ++k) stamp_put(p.stamps, rec + k, st_acc[k]);
       stamp_put(p.stamps, rec + 6, st_tiles);
-      stamp_put(p.stamps, rec + 7, st_c0);
-      stamp_put(p.stamps, rec + 8, st_r0);
       stamp_put(p.stamps, rec + 9, st_c1);
       stamp_put(p.stamps, rec + 10, st_r1);
     }
@@ -919,19 +933,14 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
   }
 
 #ifdef FFAI_STAMPS
-  // entry and exit times and the wave's hardware slot (recording workgroups, lane 0)
+  // exit times (recording workgroups, lane 0)
   auto stamp_exit = [&]() {
-    if (p.stamps && hw < p.stamp_wgs && lane == 0) {
+    if (st_rec >= 0 && lane == 0) {
       const uint64_t e1 = stamp_realtime();
       vm_wait_all();
       const uint64_t e2 = stamp_realtime();
-      const int64_t rec = ((int64_t)hw * NW + wave) * 32;
-      stamp_put(p.stamps, rec + 11, st_e0);
-      stamp_put(p.stamps, rec + 12, e1);
-      stamp_put(p.stamps, rec + 13, e2);
-      stamp_put(p.stamps, rec + 14, stamp_where());
-#pragma unroll
-      for (int k = 0; k < 3; ++k) stamp_put(p.stamps, rec + 15 + k, st_pro[k]);
+      stamp_put(p.stamps, st_rec + 12, e1);
+      stamp_put(p.stamps, st_rec + 13, e2);
     }
   };
 #endif
@@ -998,12 +1007,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
       *s_last = (done == S - 1) ? 1 : 0;
     }
     __syncthreads();
-    if (!*s_last) {
-#ifdef FFAI_STAMPS
-      stamp_exit();
-#endif
-      return;
-    }
+    if (!*s_last) return;  // (its exit is not stamped: doing so here spills registers)
     // Merge all S pieces (this one's too, as stored) in piece order, so that the result does not
     // depend on which piece finished last: KP pieces' loads in flight per round trip.
     constexpr int KP = 2;

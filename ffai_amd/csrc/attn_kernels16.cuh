@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256, 2) void fwd16_kernel(FwdParams p) {
     work = p.xcd_remap ? (hw & xm) * (p.sec1_wgs >> xs) + (hw >> xs) : hw;
     if (work >= p.sec1_work) return;
   } else {
-    const int x = hw - p.sec1_wgs, n = (int)gridDim.x - p.sec1_wgs;
+    const int x = hw - p.sec1_wgs, n = ((p.n_work - p.sec1_work + xm) >> xs) << xs;
     work = p.sec1_work + (p.xcd_remap ? (x & xm) * (n >> xs) + (x >> xs) : x);
     if (work >= p.n_work) return;
   }

@@ -424,12 +424,14 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     if (patch_end_of(kb)) patch_kt_load();
   };
 #ifdef FFAI_STAMPS
-  // event times of the workgroup, recorded by wave 0 (diagnostic builds only; attn_common.cuh)
+  // event times of the workgroup, recorded by wave 0 (diagnostic builds only; attn_common.cuh),
+  // for head_dim 64 (the head_dim-128 instantiations keep their register budget without them)
+  constexpr bool ST = D == 64;
   const int st_wg = split + p.n_split * (hk + p.Hkv * b);  // the linear workgroup index
-  const bool st_rec = p.stamps && st_wg < p.stamp_wgs && tid == 0;
-  uint64_t st_e[6];
-  const uint64_t st_r0 = stamp_realtime();
-  st_e[0] = stamp_clock();
+  const bool st_rec = ST && p.stamps && st_wg < p.stamp_wgs && tid == 0;
+  uint64_t st_e[6] = {0, 0, 0, 0, 0, 0};
+  const uint64_t st_r0 = ST ? stamp_realtime() : 0;
+  if constexpr (ST) st_e[0] = stamp_clock();
 #endif
   // The wave's first tile goes out before the Q loads: the DMA is a compiler barrier for memory
   // accesses, so nothing is outstanding when it is issued. (Issued after them, the compiler made
@@ -437,7 +439,7 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   // path, and one in-order counter covers both.)
   if (iters > 0 && t_begin + wave < t_end) issue_tile(t_begin + wave);
 #ifdef FFAI_STAMPS
-  st_e[1] = stamp_clock();
+  if constexpr (ST) st_e[1] = stamp_clock();
 #endif
   // ---- Q fragments (issued after the wave's first K/V loads): B operand of S^T, block c,
   //      contraction chunk h: d = 32 h + 8 q4 .. +7 of column 16 c + n16's row
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
     const bool patch_end = patch_end_of(kb);
     vm_wait_all();
 #ifdef FFAI_STAMPS
-    if (i == 0) st_e[2] = stamp_clock();
+    if (ST && i == 0) st_e[2] = stamp_clock();
 #endif
     if (patch_end) patch_kt_store(it);
     if (tail_dma || end_dma) {
@@ -572,8 +574,8 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
 
   // ---- merge the waves' partials through LDS (the tile area is free once all waves pass here)
 #ifdef FFAI_STAMPS
-  if (iters == 0) st_e[2] = stamp_clock();
-  st_e[3] = stamp_clock();
+  if (ST && iters == 0) st_e[2] = stamp_clock();
+  if constexpr (ST) st_e[3] = stamp_clock();
 #endif
   __syncthreads();
   float* mbase = reinterpret_cast<float*>(lds);
@@ -597,12 +599,12 @@ __global__ __launch_bounds__(NWD * 64) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 #ifdef FFAI_STAMPS
-  st_e[4] = stamp_clock();
+  if constexpr (ST) st_e[4] = stamp_clock();
   const bool st_wrote =
 #endif
   finish_unit<OUTT, D, NWD, OROW, 32, WBUF / 2>(p, mbase, b, hk, unit, split, R, tid);
 #ifdef FFAI_STAMPS
-  st_e[5] = stamp_clock();
+  if constexpr (ST) st_e[5] = stamp_clock();
   if (st_rec) {
 #pragma unroll
     for (int k = 0; k < 6; ++k) stamp_put(p.stamps, (int64_t)st_wg * 8 + k, st_e[k]);

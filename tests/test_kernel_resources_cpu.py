@@ -5,7 +5,9 @@ needs <= 256 VGPRs for two workgroups per CU, and a small change of its code can
 spill to scratch instead. The results stay correct, so no parity test notices; the kernel runs
 several times slower (an index rewrite once cost the large-v3 encoder 3x). `ffai_amd/build.py`
 writes the compiler's kernel-resource-usage remarks to `_build/resource_usage.json` at every
-build; these tests read it.
+build; these tests read it. The diagnostic library's kernels (built with FFAI_STAMPS, recorded
+under "stamps:" names) are held to the same budget, so that the phase times they record are
+those of the kernels as they run without instrumentation.
 """
 
 from __future__ import annotations
@@ -32,6 +34,7 @@ def _kernels(usage, needle):
 
 def test_report_covers_the_attention_kernels(usage):
     assert len(_kernels(usage, "fwd_kernel")) >= 40
+    assert len(_kernels(usage, "stamps:")) >= 100
     assert len(_kernels(usage, "decode_kernel")) >= 80
     for name, v in usage.items():
         assert {"vgprs", "scratch", "occupancy", "vgpr_spill"} <= set(v), name
@@ -62,11 +65,14 @@ def test_no_scalar_register_spills(usage):
     change of the code the kernels were measured with: the fused kernel has none. The decode
     kernel has none either, except its head_dim-128 K^T instantiations (no workload runs them:
     head_dim-128 decode caches keep K as rows), which park at most a few predicates of the
-    register-staging tail path (checked in their ISA)."""
-    fwd = {k: v["sgpr_spill"] for k, v in _kernels(usage, "fwd_kernel").items()
+    register-staging tail path (checked in their ISA). The diagnostic library's kernels are
+    exempt: their timers' scalar registers may be parked the same way (a few lane moves per
+    tile), while their vector registers stay within budget (the test above)."""
+    product = {k: v for k, v in usage.items() if not k.startswith("stamps:")}
+    fwd = {k: v["sgpr_spill"] for k, v in _kernels(product, "fwd_kernel").items()
            if v.get("sgpr_spill")}
     assert not fwd, fwd
-    dec = {k: v["sgpr_spill"] for k, v in _kernels(usage, "decode_kernel").items()
+    dec = {k: v["sgpr_spill"] for k, v in _kernels(product, "decode_kernel").items()
            if v.get("sgpr_spill")}
     d128_kt = {k: n for k, n in dec.items() if "ELi128ELb1E" in k}
     assert dec.keys() == d128_kt.keys(), sorted(set(dec) - set(d128_kt))
