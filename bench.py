@@ -469,17 +469,17 @@ def decode_ref_bench(torch, fa, steps, warmup, beams=5, H=16, D=64, T_enc=1500, 
     }
 
 
-def key_sweep_bench(torch, fa, sets=4, reps=20, key_lens=(1500, 3000, 4500, 6000)):
-    """Fixed and per-key cost of the fused kernel on the large-v3 layer's items: 1920 items of
-    B16 H20, 1500 query rows, bf16, K^T, with 1500 .. 6000 keys (the same items and launch
-    shape; only the key loop grows). A least-squares line through the times gives the per-key
-    rate the loops sustain and the time a launch spends outside them (prologues, epilogues,
-    the tail of the last round)."""
+def key_sweep_bench(torch, fa, B=16, H=20, sets=4, reps=20, key_lens=(1500, 3000, 4500, 6000)):
+    """Fixed and per-key cost of the fused kernel on an encoder layer's items: B x H heads of
+    1500 query rows (the large-v3 layer's 1920 items at B16 H20, whisper-small's 576 at B8 H12),
+    bf16, K^T, with 1500 .. 6000 keys (the same items and launch shape; only the key loop
+    grows). A least-squares line through the times gives the per-key rate the loops sustain and
+    the time a launch spends outside them (prologues, epilogues, the tail of the last round)."""
     import numpy as np
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(4)
-    B, H, T, D = 16, 20, 1500, 64
+    T, D = 1500, 64
     pts = []
     for tk in key_lens:
         bufs = []
@@ -541,28 +541,41 @@ def workgroup_timeline(r):
     hwid, xcc = where & 0xffffffff, where >> 32
     cu = xcc * 1000 + ((hwid >> 13) & 7) * 100 + ((hwid >> 12) & 1) * 16 + ((hwid >> 8) & 15)
     end = np.where(wrote, x2, l1)
-    gaps = []
+    span = float(end.max())
+    # each CU's two slots: a workgroup takes the slot that freed first
+    gaps, startup, loop_gaps, tail = [], [], [], []
     for c in np.unique(cu):
         idx = np.where(cu == c)[0]
         idx = idx[np.argsort(e0[idx])]
-        free = []
+        slots = []
         for i in idx:
-            if len(free) < 2:
-                free.append(end[i])
+            if len(slots) < 2:
+                slots.append([i])
                 continue
-            free.sort()
-            gaps.append(e0[i] - free.pop(0))
-            free.append(end[i])
-    span = float(end.max())
+            j = min(range(2), key=lambda k: end[slots[k][-1]])
+            gaps.append(e0[i] - end[slots[j][-1]])
+            slots[j].append(i)
+        for sl in slots:
+            startup.append(l0[sl[0]])
+            tail.append(span - end[sl[-1]])
+            loop_gaps.extend(l0[v_] - l1[u_] for u_, v_ in zip(sl[:-1], sl[1:]))
+    n_slots = 2 * len(np.unique(cu))
     return {"workgroups": int(ran.sum()), "cus": int(len(np.unique(cu))),
             "prologue_ns": med(l0 - e0), "entry_to_q_issue_ns": med(pre_q - e0),
             "q_and_tiles_issue_ns": med(issued - pre_q), "loads_land_ns": med(landed - issued),
             "barrier_ns": med(bar - landed), "first_product_ns": med(l0 - bar),
-            "loop_ns_24_tiles": med((l1 - l0)[a[:, 0, 6] == 24]),
+            "loop_tiles_most": int(a[:, 0, 6].max()),
+            "loop_ns_most_tiles": med((l1 - l0)[a[:, 0, 6] == a[:, 0, 6].max()]),
             "epilogue_issue_ns": med((x1 - l1)[wrote]), "store_ack_ns": med((x2 - x1)[wrote]),
             "exit_to_next_entry_ns": med(np.array(gaps)) if gaps else None,
             "span_ns": span,
-            "loop_share_of_slot_time": float((l1 - l0).sum() / (2 * len(np.unique(cu)) * span))}
+            # per slot (mean): first entry -> first loop, loop end -> next loop start (summed),
+            # last exit -> the launch's last exit, loops
+            "slot_startup_ns": float(np.sum(startup) / n_slots),
+            "slot_gaps_ns": float(np.sum(loop_gaps) / n_slots),
+            "slot_tail_ns": float((np.sum(tail) + (n_slots - len(startup)) * span) / n_slots),
+            "slot_loops_ns": float((l1 - l0).sum() / n_slots),
+            "loop_share_of_slot_time": float((l1 - l0).sum() / (n_slots * span))}
 
 
 def stamps_bench(torch, fa, calls=3):
@@ -579,8 +592,11 @@ def stamps_bench(torch, fa, calls=3):
         caches of <= 448 keys): each workgroup's event times from its entry (first K/V load
         issued, first tile landed, tiles done, LDS merge done, end), for the workgroups that
         wrote the output and those that only passed a split partial on.
-    Timing adds ~20% to the fused kernel (the counter reads wait for outstanding LDS reads);
-    the shares, not the absolute times, are what this leg is for. Ticks are converted with the
+    Besides, each fused-kernel workgroup's timeline (workgroup_timeline) on the large-v3 layer,
+    the whisper-small layer (B8 H12 T1500) and the Qwen2-VL-2B prefill (Hq 12 over 2 K/V heads,
+    S 4096, head_dim 128, causal, K as rows).
+    Timing adds ~8% to the fused kernel on the large-v3 layer (0.240 against 0.221 ms); the
+    shares, not the absolute times, are what this leg is for. Ticks are converted with the
     100 MHz real-time counter read beside them."""
     import ctypes
     import statistics as stats
@@ -600,7 +616,7 @@ def stamps_bench(torch, fa, calls=3):
 
     def run(q, k, v, out, rec_bytes, **kw):
         d = fa.make_desc(q, k, v, out, k_transposed=kw.get("k_transposed", False),
-                         scale=kw.get("scale", 1.0), causal=False, q_offset=0,
+                         scale=kw.get("scale", 1.0), causal=kw.get("causal", False), q_offset=0,
                          kv_lens=kw.get("kv_lens"))
         n = ctypes.c_size_t(0)
         assert lib.ffai_attn_workspace_bytes(ctypes.byref(d), ctypes.byref(n)) == 0
@@ -635,9 +651,23 @@ def stamps_bench(torch, fa, calls=3):
            "ns_per_tile": float(sums.sum() / tiles / ticks_per_ns),
            "clock_ticks_per_ns": float(ticks_per_ns)}
     enc.update(workgroup_timeline(r))
+    out_timelines = {}
+    for name, (B_, H_, Hk_, T_, D_, kt_, causal_) in (
+            ("encoder_small_layer", (8, 12, 12, 1500, 64, True, False)),
+            ("prefill_qwen2vl", (1, 12, 2, 4096, 128, False, True))):
+        q_ = torch.randn(B_, H_, T_, D_, generator=g, device=dev).bfloat16()
+        k_ = (torch.randn(B_, Hk_, D_, T_, generator=g, device=dev) if kt_ else
+              torch.randn(B_, Hk_, T_, D_, generator=g, device=dev)).bfloat16()
+        v_ = torch.randn(B_, Hk_, T_, D_, generator=g, device=dev).bfloat16()
+        o_ = torch.empty_like(q_)
+        nwg = 4096
+        r_ = run(q_, k_, v_, o_, nwg * 1024, k_transposed=kt_, scale=D_ ** -0.5,
+                 causal=causal_).reshape(nwg, 4, 32)
+        out_timelines[name] = workgroup_timeline(r_)
+        del q_, k_, v_, o_
     # ---- decode kernel, beam-5 cross- and self-attention of one whisper-medium layer
     Hd, beams, Te, cap = 16, 5, 1500, 448
-    out = {"encoder_large_v3_layer": enc}
+    out = {"encoder_large_v3_layer": enc, **out_timelines}
     qx = torch.randn(1, Hd, beams, D, generator=g, device=dev).bfloat16()
     kx = torch.randn(1, Hd, Te, D, generator=g, device=dev).bfloat16()
     vx = torch.randn(1, Hd, Te, D, generator=g, device=dev).bfloat16()
@@ -1241,24 +1271,28 @@ def main():
             + ", ".join(f"{k} WGs {v:.2f} us" for k, v in fl["read_us"].items()))
         extras["launch_floor"] = fl
     if "keys" in legs:
-        log("key sweep: the large-v3 layer's 1920 items over 1500 .. 6000 keys ...")
-        ks = key_sweep_bench(torch, fa)
-        log("key sweep: " + ", ".join(f"{p_['keys']} keys {p_['us']:.1f} us" for p_ in ks["points"])
-            + f"; per 1500 keys {ks['us_per_1500_keys']:.1f} us ({ks['loop_tflops']:.0f} TFLOP/s"
-            f" in the loops), fixed {ks['fixed_us']:.1f} us ({ks['fixed_share_at_1500']:.1%} of "
-            "the 1500-key launch)")
-        extras["key_sweep_large_v3_items"] = ks
+        for name, bb, hh in (("large_v3", 16, 20), ("small", 8, 12)):
+            log(f"key sweep: the {name} layer's items over 1500 .. 6000 keys ...")
+            ks = key_sweep_bench(torch, fa, B=bb, H=hh)
+            log(f"key sweep {name}: "
+                + ", ".join(f"{p_['keys']} keys {p_['us']:.1f} us" for p_ in ks["points"])
+                + f"; per 1500 keys {ks['us_per_1500_keys']:.1f} us ({ks['loop_tflops']:.0f} "
+                f"TFLOP/s in the loops), fixed {ks['fixed_us']:.1f} us "
+                f"({ks['fixed_share_at_1500']:.1%} of the 1500-key launch)")
+            extras[f"key_sweep_{name}_items"] = ks
     if "stamps" in legs:
         log("phase stamps: fused kernel (large-v3 layer) and decode kernel (beam-5 layer) ...")
         stp = stamps_bench(torch, fa)
         e = stp["encoder_large_v3_layer"]
         log("phase stamps: encoder " + ", ".join(f"{k} {v:.1%}" for k, v in e["share"].items())
             + f"; {e['ns_per_tile']:.0f} ns per tile per wave")
-        log("phase stamps: encoder workgroups (median ns): prologue "
-            f"{e['prologue_ns']:.0f}, loop of 24 tiles {e['loop_ns_24_tiles']:.0f}, epilogue "
-            f"{e['epilogue_issue_ns']:.0f} + ack {e['store_ack_ns']:.0f}, exit to next entry "
-            f"{e['exit_to_next_entry_ns']:.0f}; loops fill {e['loop_share_of_slot_time']:.1%} "
-            "of the slot-time")
+        for name in ("encoder_large_v3_layer", "encoder_small_layer", "prefill_qwen2vl"):
+            t = stp[name]
+            log(f"phase stamps: {name} workgroups (median ns): prologue {t['prologue_ns']:.0f}, "
+                f"loop of {t['loop_tiles_most']} tiles {t['loop_ns_most_tiles']:.0f}, epilogue "
+                f"{t['epilogue_issue_ns']:.0f} + ack {t['store_ack_ns']:.0f}; per slot: startup "
+                f"{t['slot_startup_ns']:.0f}, gaps {t['slot_gaps_ns']:.0f}, tail "
+                f"{t['slot_tail_ns']:.0f}, loops {t['slot_loops_ns']:.0f} of {t['span_ns']:.0f}")
         for name in ("decode_cross_beam5", "decode_self_beam5"):
             log(f"phase stamps: {name} {stp[name]}")
         extras["phase_stamps"] = stp
