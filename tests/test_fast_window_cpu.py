@@ -97,3 +97,19 @@ def test_f16_window_keeps_the_largest_weight_normal():
     lo, hi = window("kFastMaxLoF16", "kFastMaxHiF16")
     assert 2.0 ** lo >= 2.0 ** -14 * 2 ** 10  # keys 10 log2 units below the max stay normal
     assert 2.0 ** hi <= 65504.0                # the first subtile's weights are finite
+
+
+@pytest.mark.parametrize("dtype,inf_bits", [("bf16", 0x7F80), ("f16", 0x7C00)])
+def test_fold_overflow_test_is_exact_for_every_16_bit_pair(dtype, inf_bits):
+    """The Q fold keeps Q unscaled when a scaled half is inf or NaN. The kernels test that with
+    vector integer operations per packed pair: OR over the pairs of (y & inf_bits * 0x10001) +
+    (0x8000 - inf_bits) * 0x10001, then bits 15 and 31. Over every 16-bit value in each half,
+    that flags exactly the halves whose magnitude is at least inf_bits (an all-ones exponent),
+    and a carry never crosses from the low half into the high one."""
+    h = np.arange(1 << 16, dtype=np.uint64)
+    k2, c2 = inf_bits * 0x10001, (0x8000 - inf_bits) * 0x10001
+    for hi_vals in (h, h[::-1]):
+        y = (hi_vals << 16) | h
+        t = ((y & k2) + c2) & 0xFFFFFFFF
+        assert np.array_equal((t & 0x8000) != 0, (h & 0x7FFF) >= inf_bits), dtype
+        assert np.array_equal((t & 0x80000000) != 0, (hi_vals & 0x7FFF) >= inf_bits), dtype
