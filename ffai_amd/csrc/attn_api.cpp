@@ -625,6 +625,14 @@ int run_fwd(const ffai_attn_desc* d, const void* q, const void* k, const void* v
             int64_t(ffai::kBlockN) * d->v_strides[2] * 2 < lim;
   }
   p.scale_log2 = d->scale * 1.4426950408889634f;
+  {
+    static const bool pair_off = [] {
+      const char* e = std::getenv("FFAI_FWD_PAIR_STORE");
+      return e && e[0] == '0';
+    }();
+    p.o_pair = !pair_off && !f32 && d->out_dtype != FFAI_F32 && d->head_dim == 64 &&
+               vec_of(out, os, d->o_strides, 8) == 8;
+  }
 #ifdef FFAI_STAMPS
   p.stamps = g_stamp_buf.load();
   p.stamp_wgs = (int)std::min<size_t>(g_stamp_bytes.load() / 1024, INT32_MAX);

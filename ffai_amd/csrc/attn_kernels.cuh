@@ -1072,6 +1072,43 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     }
     if (tid == 0) __hip_atomic_store(p.counters + j, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if constexpr (OUTT != kF32 && D == 64) {
+    if (p.o_pair) {
+      // Lane (n32, g) holds d = 32dt + 8r + 4g .. +3 of its row; its partner (lane ^ 32, the same
+      // row) the other half of each 8-element run. One v_permlane32_swap per packed word hands
+      // the low lanes whole runs r = 0, 2 and the high lanes runs 1, 3: half the store
+      // instructions, each 16 bytes per lane. (Both lanes of a pair take the row test's branch
+      // alike, so every swap pairs two active lanes.)
+#pragma unroll
+      for (int c = 0; c < QW; ++c) {
+        const int qrow = q0 + 32 * c + n32;
+        if (qrow >= p.Tq) continue;
+        const float inv = l_tot[c] > 0.f ? 1.f / l_tot[c] : 0.f;
+        store_t<OUTT>* op = reinterpret_cast<store_t<OUTT>*>(p.o) + b * p.o_sb + h * p.o_sh +
+                            (int64_t)qrow * p.o_st;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int rp = 0; rp < 4; rp += 2) {
+            const f32x16& a = oacc[c][dt];
+            const uint32_t x0 = pack2<OUTT>(a[4 * rp] * inv, a[4 * rp + 1] * inv);
+            const uint32_t x1 = pack2<OUTT>(a[4 * rp + 2] * inv, a[4 * rp + 3] * inv);
+            const uint32_t y0 = pack2<OUTT>(a[4 * rp + 4] * inv, a[4 * rp + 5] * inv);
+            const uint32_t y1 = pack2<OUTT>(a[4 * rp + 6] * inv, a[4 * rp + 7] * inv);
+            // low lanes: {own x, partner's x} = run rp; high lanes: {partner's y, own y} = run
+            // rp + 1
+            const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+            *reinterpret_cast<u32x4*>(op + 32 * dt + 8 * (rp + g)) =
+                u32x4{s0[0], s1[0], s0[1], s1[1]};
+          }
+      }
+#ifdef FFAI_STAMPS
+      stamp_exit();
+#endif
+      return;
+    }
+  }
 #pragma unroll
   for (int c = 0; c < QW; ++c) {
     const int qrow = q0 + 32 * c + n32;

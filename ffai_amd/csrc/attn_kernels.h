@@ -47,6 +47,9 @@ struct FwdParams {
   int32_t dma;               // 16-bit: whole tiles may go global -> LDS by DMA (aligned, and
                              // each lane's byte offset within a K or V tile fits 32 bits)
   float scale_log2;          // scale * log2(e)
+  int32_t o_pair;            // head_dim 64, 16-bit output whose rows admit 16-byte stores: a
+                             // lane and its partner (lane ^ 32) exchange halves and store whole
+                             // 8-element runs
 #ifdef FFAI_STAMPS
   uint64_t* stamps;          // diagnostic builds only: per-wave phase times (attn_common.cuh)
   int32_t stamp_wgs;         // workgroups (by hardware index) that record them

@@ -388,3 +388,37 @@ def test_whisper_large_shape_sampled_rows(gpu):
     err = max_abs(got[bi][:, :, rows], want)
     print(f"large-v3 sampled rows: {err:.3e}")
     assert err < TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k_transposed", [True, False])
+@pytest.mark.parametrize("b,h", [(2, 3), (8, 32)])  # one-wave / four-wave x 32, four-wave x 64
+def test_16bit_output_rows_paired_and_unpaired(gpu, dtype, k_transposed, b, h):
+    """Head_dim 64 with a 16-bit output: rows that admit 16-byte stores are written by lane
+    pairs exchanging halves (whole 8-element runs); rows that do not (here a row stride of 68
+    elements: 8-byte but not 16-byte aligned) by each lane's own 4-element runs. Both carry the
+    same values, so the two outputs must agree bit for bit, and both match the oracle. 300
+    query rows: the last 32-row block is partly past the end (rows 288-299 written, 300-319
+    not)."""
+    rng = np.random.default_rng(64)
+    rnd = round_bf16 if dtype == torch.bfloat16 else round_f16
+    t, tk, d = 300, 333, 64
+    q = rnd(randn(rng, (b, h, t, d)))
+    k = rnd(randn(rng, (b, h, tk, d)))
+    v = rnd(randn(rng, (b, h, tk, d)))
+    kk = np.swapaxes(k, 2, 3) if k_transposed else k
+    qd, kd, vd = _dev(q, dtype, gpu), _dev(kk, dtype, gpu), _dev(v, dtype, gpu)
+    paired = torch.empty(b, h, t, d, dtype=dtype, device=gpu)
+    wide = torch.full((b, h, t, 68), 7.0, dtype=dtype, device=gpu)  # 68: 136-byte rows
+    unpaired = wide[..., :d]
+    if b == 8:
+        assert fa.plan(qd, kd, vd, paired, k_transposed=k_transposed,
+                       scale=0.125)["shape"] == "wave4x2"
+    for out in (paired, unpaired):
+        fa.attention(qd, kd, vd, k_transposed=k_transposed, scale=0.125, out=out)
+    assert torch.equal(paired.view(torch.int16), unpaired.contiguous().view(torch.int16))
+    assert torch.all(wide[..., d:] == 7.0)  # nothing written past each row's 64 elements
+    want = oracle.attend_general(q, k, v, k_transposed=False, scale=0.125)
+    err = max_abs(_host(paired), want)
+    print(f"16-bit output rows {dtype} kt={k_transposed}: {err:.3e}")
+    assert err < TOL_BF16
