@@ -566,13 +566,6 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
     } else {
       constexpr uint32_t kInfBits = MODE == kBF16 ? 0x7f80u : 0x7c00u;
       u32x4 qs[QW][D / 16];
-      // Bit 15 (31) of ovf ends up set when the low (high) half of some scaled pair has an all-ones
-      // exponent (inf or NaN): that half's exponent bits plus the increment that carries an
-      // all-ones exponent into bit 15, OR-ed over the pairs; vector operations only, no chain of
-      // compares into scalar registers.
-      constexpr uint32_t kExp2 = kInfBits * 0x10001u;
-      constexpr uint32_t kCarry2 = (0x8000u - kInfBits) * 0x10001u;
-      uint32_t ovf = 0u;
 #pragma unroll
       for (int c = 0; c < QW; ++c)
 #pragma unroll
@@ -581,13 +574,26 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && (D == 64 || MODE != kF32)) ? 2
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const uint32_t w = qf[c][s][k];
-            const uint32_t y =
-                pack2<MODE>(to_f32<MODE>(w & 0xffffu) * sl2, to_f32<MODE>(w >> 16) * sl2);
-            ovf |= (y & kExp2) + kCarry2;
-            w4[k] = y;
+            w4[k] = pack2<MODE>(to_f32<MODE>(w & 0xffffu) * sl2, to_f32<MODE>(w >> 16) * sl2);
           }
           qs[c][s] = u32x4{w4[0], w4[1], w4[2], w4[3]};
         }
+      // Only a factor above 1 can carry a finite element past the type's largest (below it the
+      // product rounds to at most the input's magnitude; an inf or NaN input stays one either
+      // way). Then bit 15 (31) of ovf ends up set when the low (high) half of some scaled pair
+      // has an all-ones exponent: that half's exponent bits plus the increment that carries an
+      // all-ones exponent into bit 15, OR-ed over the pairs (vector operations only).
+      uint32_t ovf = 0u;
+      if (sl2 > 1.f) {
+        constexpr uint32_t kExp2 = kInfBits * 0x10001u;
+        constexpr uint32_t kCarry2 = (0x8000u - kInfBits) * 0x10001u;
+#pragma unroll
+        for (int c = 0; c < QW; ++c)
+#pragma unroll
+          for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ovf |= (qs[c][s][k] & kExp2) + kCarry2;
+      }
       if (__builtin_amdgcn_ballot_w64((ovf & 0x80008000u) != 0u) == 0) {
 #pragma unroll
         for (int c = 0; c < QW; ++c)

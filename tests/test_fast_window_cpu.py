@@ -113,3 +113,26 @@ def test_fold_overflow_test_is_exact_for_every_16_bit_pair(dtype, inf_bits):
         t = ((y & k2) + c2) & 0xFFFFFFFF
         assert np.array_equal((t & 0x8000) != 0, (h & 0x7FFF) >= inf_bits), dtype
         assert np.array_equal((t & 0x80000000) != 0, (hi_vals & 0x7FFF) >= inf_bits), dtype
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_fold_by_at_most_one_keeps_every_finite_element_finite(dtype):
+    """The kernels test the folded Q for inf/NaN only when scale * log2(e) exceeds 1: below,
+    every finite 16-bit value times the factor (an f32 product, rounded to nearest-even to the
+    16-bit type) stays finite. Checked for every finite value of the type and factors up to 1."""
+    from tests.helpers import round_f16
+
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    if dtype == "bf16":
+        vals = (bits << 16).view(np.float32)
+        rnd = round_bf16
+    else:
+        vals = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+        rnd = round_f16
+    vals = vals[np.isfinite(vals)]
+    for f in (1.0, np.nextafter(np.float32(1.0), np.float32(0.0)), 0.5, 0.18033688, 1e-3):
+        with np.errstate(over="ignore"):
+            out = rnd(vals * np.float32(f))
+        assert np.isfinite(out).all(), (dtype, f)
+    with np.errstate(over="ignore"):  # and just above 1 a finite value can overflow
+        assert not np.isfinite(rnd(vals * np.float32(1.0078125))).all()
