@@ -145,6 +145,9 @@ def load():
     L.ffai_encoder_attn_fwd.argtypes = [ed, vp, ew, vp, vp, ctypes.c_size_t, vp]
     L.ffai_gemv_f16.argtypes = [vp, i32, i32, vp, i32, i64, vp, i64, vp]
     L.ffai_gemv_f16_qkv_cache.argtypes = [vp, vp, i32, vp, i32, i64, vp, i64, cp, vp]
+    ip = ctypes.POINTER(ctypes.c_int32)
+    L.ffai_gemv_f16_plan_info.argtypes = [i32, i32, i32, ip, ip, ip, ip,
+                                          ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_vocab_int8_quantize.argtypes = [vp, i32, i32, i32, i32, vp, vp, vp, vp]
     L.ffai_vocab_int8_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_size_t)]
     L.ffai_vocab_int8_logits.argtypes = [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, i64, vp,
@@ -161,11 +164,22 @@ def load():
                  "ffai_attend_merged_workspace_bytes", "ffai_kv_append", "ffai_kv_gather",
                  "ffai_kv_advance", "ffai_gemv_f16_qkv_cache",
                  "ffai_cross_kv_build", "ffai_encoder_attn_workspace_bytes",
-                 "ffai_encoder_attn_fwd", "ffai_gemv_f16", "ffai_vocab_int8_quantize",
+                 "ffai_encoder_attn_fwd", "ffai_gemv_f16", "ffai_gemv_f16_plan_info",
+                 "ffai_vocab_int8_quantize",
                  "ffai_vocab_int8_workspace_bytes", "ffai_vocab_int8_logits"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
+
+
+def gemv_plan_info(out_dim: int, in_dim: int, rows: int) -> dict:
+    """The launch shape ffai_gemv_f16 uses for (out_dim, in_dim, rows)."""
+    v = [ctypes.c_int32() for _ in range(4)]
+    lds = ctypes.c_size_t()
+    check(load().ffai_gemv_f16_plan_info(out_dim, in_dim, rows, *[ctypes.byref(a) for a in v],
+                                         ctypes.byref(lds)))
+    return {"tile_rows": v[0].value, "waves": v[1].value, "blocks_per_wave": v[2].value,
+            "passes": v[3].value, "lds_bytes": lds.value}
 
 
 def plan_info(desc: AttnDesc) -> dict:

@@ -18,89 +18,48 @@
 namespace ffai {
 namespace {
 
-// Sum over the wave's 64 lanes in VALU cross-lane moves (DPP), no LDS permutes: within each
-// 16-lane row by quad permutes and row rotations, then rows 0-3 folded into lane 63 by the row
-// broadcasts of lanes 15 and 31 (lanes without a source add 0); the total is read from lane 63.
-__device__ __forceinline__ float dpp_add(float v, int x) { return v + __builtin_bit_cast(float, x); }
-__device__ __forceinline__ float wave_sum(float v) {
-  auto mv = [](float a, auto ctrl) {
-    return __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), decltype(ctrl)::value, 0xf,
-                                       0xf, false);
-  };
-  v = dpp_add(v, mv(v, std::integral_constant<int, 0xb1>{}));   // quad_perm [1,0,3,2]
-  v = dpp_add(v, mv(v, std::integral_constant<int, 0x4e>{}));   // quad_perm [2,3,0,1]
-  v = dpp_add(v, mv(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
-  v = dpp_add(v, mv(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
-  v = dpp_add(v, mv(v, std::integral_constant<int, 0x142>{}));  // row_bcast:15
-  v = dpp_add(v, mv(v, std::integral_constant<int, 0x143>{}));  // row_bcast:31
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-// ---- f16 GEMV ---------------------------------------------------------------------------------
-// A workgroup of 4 waves, one output row per wave: lane l takes the row's 16-byte weight chunks
-// l, l + 64, ... (coalesced along the row, four in flight per lane), widens them to f32 and
-// multiplies them with every beam's x, read straight from global memory (the few KB of x stay
-// in L2; staging them in LDS behind a barrier put a second dependent round trip in front of the
-// weight loads), then the wave reduces each beam's sum.
-// Lane partial sums of output row `wr` with every beam's x (the wave sums them afterwards).
-template <int R>
-__device__ __forceinline__ void gemv_row(const uint16_t* __restrict__ wr, int in_dim,
-                                         const float* __restrict__ x, int rows, int64_t xs,
-                                         int lane, float (&acc)[R]) {
-  const int chunks = in_dim / 8;
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  constexpr int kBatch = 4;  // weight chunks in flight per lane
-  for (int c0 = lane; c0 < chunks; c0 += 64 * kBatch) {
-    u32x4 wv[kBatch];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int c = min(c0 + 64 * j, chunks - 1);
-      wv[j] = ld16(wr + 8 * c);
-    }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int c = c0 + 64 * j;
-      if (c >= chunks) break;
-      float wf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        wf[2 * e] = to_f32<kF16>(wv[j][e] & 0xffffu);
-        wf[2 * e + 1] = to_f32<kF16>(wv[j][e] >> 16);
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        // beams past `rows` repeat the last one's x (R is the compiled width); never stored
-        const float* xr = x + min(r, rows - 1) * xs + 8 * c;
-        const f32x4 a = *reinterpret_cast<const f32x4*>(xr);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(xr + 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[r] = __builtin_fmaf(wf[e], a[e], acc[r]);
-          acc[r] = __builtin_fmaf(wf[4 + e], b[e], acc[r]);
-        }
-      }
-    }
-  }
-}
-
-template <int R>
-__global__ __launch_bounds__(256) void gemv_f16_kernel(const uint16_t* __restrict__ w,
-                                                       int out_dim, int in_dim,
-                                                       const float* __restrict__ x, int rows,
-                                                       int64_t xs, float* __restrict__ y,
-                                                       int64_t ys) {
-  const int tid = item_id(), lane = tid & 63, wave = tid >> 6;
-  const int o = wg_id_x() * 4 + wave;
-  if (o >= out_dim) return;
-  float acc[R];
-  gemv_row<R>(w + (int64_t)o * in_dim, in_dim, x, rows, xs, lane, acc);
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float v = wave_sum(acc[r]);
-    if (lane == r && r < rows) y[r * ys + o] = v;
-  }
-}
+// ---- f16 GEMV on the matrix cores ------------------------------------------------------------
+// y = W x for up to 16 beams as v_mfma_f32_16x16x32_f16 tiles: the weights are the A operand,
+// loaded from HBM straight into the operand layout (lane l: row l % 16, eight consecutive
+// elements at 8 (l / 16) of each 32-element block), and the beams are the B operand's columns.
+// A one-row-per-wave VALU design reads every beam's x chunk again beside each 16-byte weight
+// chunk (ten x loads per weight load at five beams), and those loads, not the weights, set its
+// time; here x is read once per wave and shared by all the tile's rows.
+//
+// Tiles of TR weight rows, TR a power of two >= rows: MFMA row m = q TR + r holds weight row r
+// over K part q, column n = q TR + b holds beam b over the same part (QN = 16 / TR parts), and
+// the diagonal blocks C[q TR + r][q TR + b] are the parts' sums (the other blocks are computed
+// and discarded: the matrix core has time to spare, HBM does not). Smaller tiles give short
+// outputs more workgroups. A workgroup of NW waves owns one tile over the whole K: wave w takes
+// 32 NJ elements of every part per pass; the waves' partial tiles meet in LDS and are summed in
+// a fixed order, so every call gives the same bits.
+//
+// x to f16 without losing precision: per (column, wave, pass), x is scaled by a power of two s
+// that brings max |x| into [2^14, 2^15), and split into hi = f16(x s) and lo = f16(x s - hi)
+// (x s - hi is exact in f32). hi + lo carries x s to 22 significant bits; the f16 x f16
+// products are exact in f32 and sum in f32; the tile is then multiplied by 1/s (exact). Elements
+// more than 2^28 below their column's maximum fall into f16's subnormal range (absolute error
+// below 2^-39 of the maximum). A column range holding an infinite element keeps its hi halves
+// only (lo = 0, where inf - inf would give NaN), so an infinite x gives the infinite products
+// f32 arithmetic gives.
+//
+// Loads: x first (dense: consecutive lanes take consecutive 16-byte pieces of each column's
+// range, so every lane of the load is used), then the weights; loads complete in issue order,
+// so the split of x runs while the weights are in flight. The split values reach the B layout
+// through the wave's own LDS region (no workgroup barrier). Every load reads a clamped, valid
+// address unconditionally and out-of-range elements are zeroed by a select afterwards (a load
+// on one side of a branch makes the compiler wait for all loads at the join).
+struct GemvParams {
+  const uint16_t* w;
+  const float* x;
+  int64_t xs;
+  float* y;
+  int64_t ys;
+  int32_t out_dim, in_dim, rows;
+  int32_t tr_log2;  // tile rows TR = 1 << tr_log2
+  int32_t nw;       // waves per workgroup
+  int32_t passes;   // K passes of QN * nw * 32 NJ elements
+};
 
 // The self-attention q/k/v projection of a decode step with the new K/V rows written straight
 // into the layer's cache: weights packed (q; k; v), n = heads * head_dim outputs each. Output o
@@ -119,63 +78,255 @@ struct QkvCacheParams {
   int32_t n, head_dim, capacity;
 };
 
-template <int R, int CDT>
-__global__ __launch_bounds__(256) void gemv_f16_qkv_kernel(const uint16_t* __restrict__ w,
-                                                           int in_dim,
-                                                           const float* __restrict__ x, int rows,
-                                                           int64_t xs, QkvCacheParams p) {
-  const int tid = item_id(), lane = tid & 63, wave = tid >> 6;
-  const int o = wg_id_x() * 4 + wave;
-  if (o >= 3 * p.n) return;
-  float acc[R];
-  gemv_row<R>(w + (int64_t)o * in_dim, in_dim, x, rows, xs, lane, acc);
-  const int part = o / p.n;  // 0: q, 1: k, 2: v
-  const int oo = o - part * p.n;
-  const int h = oo / p.head_dim, d = oo - h * p.head_dim;
+// Max over groups of G consecutive lanes (G = 8, 16 or 32; every lane gets its group's max).
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  v = fmaxf(v, dpp_mov<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror: the other quad of the 8
+  if constexpr (G >= 16) v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror: the other 8 of the 16
+  if constexpr (G >= 32) {
+    const uint32_t u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // lanes l and l ^ 16
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  return v;
+}
+
+// EPI 0: y[b][o] = sum. EPI 1: the q/k/v epilogue, cache elements of type CDT.
+// TL >= 0: a specialized launch shape known at compile time (tile rows 1 << TL, NW waves, one
+// pass, the first NXL dense x loads hold every beam); the compiler then folds the index
+// arithmetic and unrolls the waves' reduction (~0.3-0.8 us per call at the decoder's shapes).
+// TL < 0: the shape comes from the parameters.
+template <int NJ, int EPI, int CDT, int TL = -1, int NW = 0, int NXL = 0>
+__global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCacheParams qp) {
+  constexpr bool SPEC = TL >= 0;
+  constexpr int KW = 32 * NJ;  // elements of one part per wave and pass
+  constexpr int RS = KW + 8;   // LDS row of a column (halves; 16 bytes of it hold the scale)
+  constexpr int LPC = KW / 4;  // lanes per column in the dense x load
+  constexpr int NI = LPC / 4;  // dense x loads for all 16 columns
+  extern __shared__ __attribute__((aligned(16))) uint16_t gemv_lds[];
+  const int tid = item_id(), lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tl = SPEC ? TL : p.tr_log2, tr = 1 << tl, qn = 16 >> tl;
+  const int nw = SPEC ? NW : p.nw;
+  const int kp = nw * KW;  // one part's elements per pass
+  const int m = lane & 15, g = lane >> 4;
+  const int q = m >> tl, r = m & (tr - 1);  // A row m: weight row r of part q
+  const int tile = wg_id_x();
+  const uint16_t* wr = p.w + (int64_t)min(tile * tr + r, p.out_dim - 1) * p.in_dim;
+  uint16_t* xw = gemv_lds + wave * (32 * RS);  // this wave's hi rows [16][RS], then lo rows
+  const bool nv = (m & (tr - 1)) < p.rows;  // B column m holds a beam
+  const int ni = (qn * p.rows * LPC + 63) / 64;  // dense x loads that hold a beam
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int ps = 0; ps < (SPEC ? 1 : p.passes); ++ps) {
+    const int kb = ps * qn * kp + wave * KW;
+    // Dense x: load slot v = 0..15 is beam v / QN over part v % QN (column n = part TR + beam),
+    // LPC lanes per slot, 4 elements each. Slots of beams >= rows load a valid beam's elements
+    // and fill LDS rows that are never read; no branch, no division.
+    f32x4 xv[NI];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float v = wave_sum(acc[r]);
-    if (p.bias) v = v + p.bias[o];
-    if (lane == r && r < rows) {
+    for (int i = 0; i < NI; ++i) {
+      if (SPEC && i >= NXL) break;
+      const int f = 64 * i + lane, v = f / LPC;
+      const int b = min(v >> (4 - tl), p.rows - 1), part = v & (qn - 1);
+      const int k = min(kb + part * kp + 4 * (f % LPC), p.in_dim - 4);
+      xv[i] = *reinterpret_cast<const f32x4*>(p.x + b * p.xs + k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 a[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      a[j] = ld16(wr + min(kb + q * kp + 32 * j + 8 * g, p.in_dim - 8));
+    // split the loaded slots that hold a beam (the first QN * rows; the rest are never read)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      if (SPEC ? i >= NXL : i >= ni) break;  // wave-uniform
+      const int f = 64 * i + lane, v = f / LPC, c4 = f % LPC;
+      const int b = v >> (4 - tl), part = v & (qn - 1);
+      const bool ok = kb + part * kp + 4 * c4 < p.in_dim;
+      float mx = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[i][e] = ok ? xv[i][e] : 0.f;
+        mx = fmaxf(mx, fabsf(xv[i][e]));
+      }
+      mx = group_max<LPC>(mx);
+      // s = 2^(14 - e) for max in [2^e, 2^(e+1)): biased exponent 141 - e = 268 - (max >> 23),
+      // kept in [1, 253] so that s and 1/s are normal
+      const int sb = min(max(268 - (int)(__float_as_uint(mx) >> 23), 1), 253);
+      const float sc = __uint_as_float((uint32_t)sb << 23);
+      const bool fin = mx < __builtin_inff();  // an infinite element: its column keeps hi only
+      uint32_t hp[2], lp[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v0 = xv[i][2 * e] * sc, v1 = xv[i][2 * e + 1] * sc;
+        const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+        const _Float16 l0 = (_Float16)(v0 - (float)h0), l1 = (_Float16)(v1 - (float)h1);
+        hp[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        lp[e] = fin ? (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16)
+                    : 0u;
+      }
+      const int n = (part << tl) + b;
+      *reinterpret_cast<u32x2*>(xw + n * RS + 4 * c4) = u32x2{hp[0], hp[1]};
+      *reinterpret_cast<u32x2*>(xw + (16 + n) * RS + 4 * c4) = u32x2{lp[0], lp[1]};
+      if (c4 == 0) xw[n * RS + KW] = (uint16_t)sb;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      u32x4 bh = {0u, 0u, 0u, 0u}, bl = bh;
+      if (nv) {
+        bh = ld16(xw + m * RS + 32 * j + 8 * g);
+        bl = ld16(xw + (16 + m) * RS + 32 * j + 8 * g);
+      }
+      const bool kin = kb + q * kp + 32 * j + 8 * g < p.in_dim;
+      u32x4 aj;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) aj[e] = kin ? a[j][e] : 0u;
+      c = mfma16x16<kF16>(aj, bh, c);
+      c = mfma16x16<kF16>(aj, bl, c);
+    }
+    // D lane l holds rows 4 (l / 16) .. +3 of column l % 16 = m: the column's 1/s
+    const int sb = nv ? (int)xw[m * RS + KW] : 127;
+    const float inv = __uint_as_float((uint32_t)(254 - sb) << 23);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(c[e], inv, acc[e]);
+    // the next pass rewrites this region: its reads are done (one wave's LDS accesses complete
+    // in order)
+  }
+  // the waves' partial tiles, each in its own region: sum over parts and waves in a fixed order
+  reinterpret_cast<f32x4*>(xw)[lane] = acc;
+  __syncthreads();
+  for (int t = tid; t < (p.rows << tl); t += nw * 64) {
+    const int b = t >> tl, rr = t & (tr - 1);  // beam b, tile row rr
+    const int o = tile * tr + rr;
+    if (o >= p.out_dim) continue;
+    float v = 0.f;
+    for (int qq = 0; qq < qn; ++qq) {
+      const int mm = (qq << tl) + rr, nn = (qq << tl) + b;
+      const int l = nn + 16 * (mm >> 2), e = mm & 3;
+      // all the waves' values first (independent LDS reads), then the sum in wave order
+      float pv[16];
+#pragma unroll
+      for (int ww = 0; ww < 16; ++ww)
+        pv[ww] = ww < nw ? reinterpret_cast<const float*>(gemv_lds + ww * (32 * RS))[4 * l + e]
+                           : 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 16; ++ww) v += pv[ww];
+    }
+    if constexpr (EPI == 0) {
+      p.y[b * p.ys + o] = v;
+    } else {
+      if (qp.bias) v = v + qp.bias[o];
+      const int part = o / qp.n;  // 0: q, 1: k, 2: v
+      const int oo = o - part * qp.n;
       if (part == 0) {
-        p.q[r * p.qs + oo] = v;
+        qp.q[b * qp.qs + oo] = v;
       } else {
         // a length outside [1, capacity] is clamped; 0 (no advance) writes nothing
-        const int pos = min(max(p.lens[r], 0), p.capacity) - 1;
+        const int pos = min(max(qp.lens[b], 0), qp.capacity) - 1;
         if (pos >= 0) {
-          store_t<CDT>* c = reinterpret_cast<store_t<CDT>*>(part == 1 ? p.ck : p.cv) +
-                            (int64_t)r * p.cs + (int64_t)h * p.ch + (int64_t)pos * p.cp + d;
-          if constexpr (CDT == kF32) *c = v;
-          else *c = from_f32<CDT>(v);
+          const int h = oo / qp.head_dim, d = oo - h * qp.head_dim;
+          store_t<CDT>* cptr = reinterpret_cast<store_t<CDT>*>(part == 1 ? qp.ck : qp.cv) +
+                               (int64_t)b * qp.cs + (int64_t)h * qp.ch + (int64_t)pos * qp.cp + d;
+          if constexpr (CDT == kF32) *cptr = v;
+          else *cptr = from_f32<CDT>(v);
         }
       }
     }
   }
 }
 
-template <int R>
-hipError_t launch_gemv_any(const uint16_t* w, int out_dim, int in_dim, const float* x, int rows,
-                           int64_t xs, float* y, int64_t ys, hipStream_t st) {
-  const unsigned grid = (unsigned)((out_dim + 3) / 4);
-  hipLaunchKernelGGL((gemv_f16_kernel<R>), dim3(grid), dim3(256), 0, st, w, out_dim,
-                     in_dim, x, rows, xs, y, ys);
+// Launch shape for (out_dim, in_dim, rows): the largest tile (<= 16 rows, >= rows) that still
+// gives ~192 workgroups, then per part the fewest passes with at most 16 waves, 32 NJ elements
+// each (NJ 2 or 4; 1 for a single block).
+struct GemvShape {
+  int tr_log2, nw, nj, passes;
+  size_t lds;
+};
+GemvShape gemv_shape(int out_dim, int in_dim, int rows) {
+  int min_tl = 0;
+  while ((1 << min_tl) < rows) ++min_tl;
+  int tl = 4;
+  while (tl > min_tl && (out_dim + (1 << tl) - 1) / (1 << tl) < 192) --tl;
+  const int qn = 16 >> tl;
+  const int bpp = (in_dim / 8 + 4 * qn - 1) / (4 * qn);  // 32-element blocks per part
+  GemvShape s{};
+  s.tr_log2 = tl;
+  s.nj = bpp == 1 ? 1 : (bpp + 1) / 2 <= 16 ? 2 : 4;
+  s.nw = std::min(16, (bpp + s.nj - 1) / s.nj);
+  s.passes = (bpp + s.nw * s.nj - 1) / (s.nw * s.nj);
+  s.lds = (size_t)s.nw * 64 * (32 * s.nj + 8);
+  return s;
+}
+
+// One kernel instance on its launch shape; dynamic LDS above 64 KB is allowed once per instance
+// (up to the CU's 160 KB).
+template <typename K>
+hipError_t launch_one(K kern, size_t lds, dim3 grid, dim3 block, hipStream_t st,
+                      const GemvParams& p, const QkvCacheParams& qp) {
+  if (lds > 65536) {
+    static const hipError_t allowed = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+        160 * 1024);
+    if (allowed != hipSuccess) return allowed;
+  }
+  hipLaunchKernelGGL(kern, grid, block, lds, st, p, qp);
   return hipGetLastError();
 }
 
-template <int R>
-hipError_t launch_qkv_cache(const uint16_t* w, int in_dim, const float* x, int rows, int64_t xs,
-                            const QkvCacheParams& p, int cdt, hipStream_t st) {
-  const unsigned grid = (unsigned)((3 * p.n + 3) / 4);
-  if (cdt == kF32)
-    hipLaunchKernelGGL((gemv_f16_qkv_kernel<R, kF32>), dim3(grid), dim3(256), 0, st, w, in_dim, x,
-                       rows, xs, p);
-  else if (cdt == kF16)
-    hipLaunchKernelGGL((gemv_f16_qkv_kernel<R, kF16>), dim3(grid), dim3(256), 0, st, w, in_dim, x,
-                       rows, xs, p);
-  else
-    hipLaunchKernelGGL((gemv_f16_qkv_kernel<R, kBF16>), dim3(grid), dim3(256), 0, st, w, in_dim,
-                       x, rows, xs, p);
-  return hipGetLastError();
+// The specialized shape (TL, NW, NJ, NXL) if the call's shape is it and its beams fit NXL loads.
+template <int EPI, int CDT, int TL, int NW, int NJ, int NXL>
+bool try_spec(const GemvShape& s, int nxl, dim3 grid, hipStream_t st, const GemvParams& p,
+              const QkvCacheParams& qp, hipError_t& e) {
+  if (s.tr_log2 != TL || s.nw != NW || s.nj != NJ || s.passes != 1 || nxl > NXL) return false;
+  e = launch_one(gemv_f16_kernel<NJ, EPI, CDT, TL, NW, NXL>, s.lds, grid, dim3(64 * NW), st, p,
+                 qp);
+  return true;
+}
+
+template <int EPI, int CDT>
+hipError_t launch_gemv(GemvParams p, const QkvCacheParams& qp, int out_rows, hipStream_t st) {
+  const GemvShape s = gemv_shape(out_rows, p.in_dim, p.rows);
+  p.tr_log2 = s.tr_log2;
+  p.nw = s.nw;
+  p.passes = s.passes;
+  const dim3 grid((unsigned)((out_rows + (1 << s.tr_log2) - 1) >> s.tr_log2));
+  // dense x loads that hold a beam: (16 >> tl) parts x rows columns, 8 NJ lanes each
+  const int nxl = ((16 >> s.tr_log2) * p.rows * 8 * s.nj + 63) / 64;
+  hipError_t e = hipSuccess;
+  // the whisper decoders' projections, beam 5 and greedy: medium (d 1024: n x n, 3n x n, 4n x n,
+  // n x 4n) and large (d 1280)
+  if constexpr (EPI == 0) {
+    if (try_spec<EPI, CDT, 3, 8, 2, 3>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 8, 2, 4>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 2>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 4>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 16, 4, 5>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 16, 4, 8>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 2, 4, 2, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 2, 16, 2, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 10, 2, 3>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 10, 4, 3>(s, nxl, grid, st, p, qp, e))
+      return e;
+  } else {
+    if (try_spec<EPI, CDT, 4, 16, 2, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 2>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 4>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 10, 4, 3>(s, nxl, grid, st, p, qp, e))
+      return e;
+  }
+  const dim3 block(64 * s.nw);
+  if (s.nj == 1) return launch_one(gemv_f16_kernel<1, EPI, CDT>, s.lds, grid, block, st, p, qp);
+  if (s.nj == 2) return launch_one(gemv_f16_kernel<2, EPI, CDT>, s.lds, grid, block, st, p, qp);
+  return launch_one(gemv_f16_kernel<4, EPI, CDT>, s.lds, grid, block, st, p, qp);
 }
 
 // ---- int8 vocabulary projection -------------------------------------------------------------
@@ -328,21 +479,30 @@ int ffai_gemv_f16(const void* w, int32_t out_dim, int32_t in_dim, const float* x
   if ((int64_t)out_dim * in_dim >= (int64_t(1) << 40)) return api_fail(FFAI_ERR_INVALID, "weights too large");
   const int rc = api_check_device();
   if (rc != FFAI_OK) return rc;
-  const auto* wp = static_cast<const uint16_t*>(w);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  switch (rows) {
-    case 1: e = launch_gemv_any<1>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 2: e = launch_gemv_any<2>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 3: e = launch_gemv_any<3>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 4: e = launch_gemv_any<4>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 5: e = launch_gemv_any<5>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 6: e = launch_gemv_any<6>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 7: e = launch_gemv_any<7>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    case 8: e = launch_gemv_any<8>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-    default: e = launch_gemv_any<16>(wp, out_dim, in_dim, x, rows, x_row_stride, y, y_row_stride, st); break;
-  }
+  GemvParams p{};
+  p.w = static_cast<const uint16_t*>(w);
+  p.x = x; p.xs = x_row_stride; p.y = y; p.ys = y_row_stride;
+  p.out_dim = out_dim; p.in_dim = in_dim; p.rows = rows;
+  const hipError_t e = launch_gemv<0, kF32>(p, QkvCacheParams{}, out_dim,
+                                            static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
+  return FFAI_OK;
+}
+
+int ffai_gemv_f16_plan_info(int32_t out_dim, int32_t in_dim, int32_t rows, int32_t* tile_rows,
+                            int32_t* waves, int32_t* blocks_per_wave, int32_t* passes,
+                            size_t* lds_bytes) {
+  api_clear_error();
+  if (!tile_rows || !waves || !blocks_per_wave || !passes || !lds_bytes)
+    return api_fail(FFAI_ERR_INVALID, "null pointer");
+  if (out_dim < 1 || in_dim < 8 || in_dim % 8) return api_fail(FFAI_ERR_INVALID, "out_dim >= 1 and in_dim a multiple of 8");
+  if (rows < 1 || rows > kMaxGemvRows) return api_fail(FFAI_ERR_INVALID, "rows must be in [1, 16]");
+  const GemvShape s = gemv_shape(out_dim, in_dim, rows);
+  *tile_rows = 1 << s.tr_log2;
+  *waves = s.nw;
+  *blocks_per_wave = s.nj;
+  *passes = s.passes;
+  *lds_bytes = s.lds;
   return FFAI_OK;
 }
 
@@ -377,21 +537,15 @@ int ffai_gemv_f16_qkv_cache(const void* w, const float* bias, int32_t in_dim, co
   p.ck = c->k; p.cv = c->v; p.lens = c->lens;
   p.cs = c->strides[0]; p.ch = c->strides[1]; p.cp = c->strides[2];
   p.n = (int32_t)n; p.head_dim = c->head_dim; p.capacity = c->capacity;
-  const auto* wp = static_cast<const uint16_t*>(w);
+  GemvParams gp{};
+  gp.w = static_cast<const uint16_t*>(w);
+  gp.x = x; gp.xs = x_row_stride;
+  gp.out_dim = (int32_t)(3 * n); gp.in_dim = in_dim; gp.rows = rows;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int cdt = c->dtype;  // FFAI_F32 / F16 / BF16 are kF32 / kF16 / kBF16
-  hipError_t e;
-  switch (rows) {
-    case 1: e = launch_qkv_cache<1>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 2: e = launch_qkv_cache<2>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 3: e = launch_qkv_cache<3>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 4: e = launch_qkv_cache<4>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 5: e = launch_qkv_cache<5>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 6: e = launch_qkv_cache<6>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 7: e = launch_qkv_cache<7>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    case 8: e = launch_qkv_cache<8>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-    default: e = launch_qkv_cache<16>(wp, in_dim, x, rows, x_row_stride, p, cdt, st); break;
-  }
+  const hipError_t e = cdt == kF32   ? launch_gemv<1, kF32>(gp, p, (int)(3 * n), st)
+                       : cdt == kF16 ? launch_gemv<1, kF16>(gp, p, (int)(3 * n), st)
+                                     : launch_gemv<1, kBF16>(gp, p, (int)(3 * n), st);
   if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
   return FFAI_OK;
 }

@@ -29,11 +29,24 @@ extern "C" {
 /* y[r][o] = sum_i W[o][i] * x[r][i] for r < rows: W (out_dim, in_dim) f16 row-major (the
  * layout QLinear stores, F16Gemv::new, f16_gemv.rs:88-115), x f32 rows (row stride
  * x_row_stride), y f32 rows (row stride y_row_stride). in_dim a multiple of 8 (the reference's
- * decline rule, :101-103), rows <= 16. Products in f32 (F16Gemv::forward / dot_f16,
- * :117-196); the summation order differs from the reference's 16-lane AVX order, so results
- * agree to f32 rounding, not bit for bit. */
+ * decline rule, :101-103), rows <= 16. The reference multiplies and adds in f32
+ * (F16Gemv::forward / dot_f16, :117-196). Here the products run on the matrix cores: each x
+ * element is scaled by a power of two and carried as the sum of two f16 values (22 significant
+ * bits), the f16 x f16 products are exact in f32 and sum in f32, in another order than the
+ * reference's 16-lane AVX order; results agree to f32 rounding, not bit for bit. A call gives
+ * the same bits every time. An infinite x gives the infinite sums f32 arithmetic gives; an
+ * infinite weight can give NaN where f32 arithmetic gives +-inf (it also multiplies x's low
+ * half, which may be 0). */
 int ffai_gemv_f16(const void* w, int32_t out_dim, int32_t in_dim, const float* x, int32_t rows,
                   int64_t x_row_stride, float* y, int64_t y_row_stride, void* stream);
+
+/* Launch shape ffai_gemv_f16 and ffai_gemv_f16_qkv_cache (with out_dim = 3 * heads * head_dim)
+ * choose for (out_dim, in_dim, rows): weight rows per tile (workgroup), waves per workgroup,
+ * 32-element blocks per wave and pass, passes over in_dim, and dynamic LDS bytes. A diagnostic
+ * query with no counterpart in the reference. */
+int ffai_gemv_f16_plan_info(int32_t out_dim, int32_t in_dim, int32_t rows, int32_t* tile_rows,
+                            int32_t* waves, int32_t* blocks_per_wave, int32_t* passes,
+                            size_t* lds_bytes);
 
 /* The self-attention q/k/v projection of a decode step, with the new K/V rows written straight
  * into the layer's cache: replaces, for single-token steps, the three GEMVs of forward_self

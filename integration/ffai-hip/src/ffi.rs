@@ -178,6 +178,9 @@ extern "C" {
     pub fn ffai_gemv_f16(w: *const c_void, out_dim: i32, in_dim: i32, x: *const f32, rows: i32,
                          x_row_stride: i64, y: *mut f32, y_row_stride: i64,
                          stream: *mut c_void) -> c_int;
+    pub fn ffai_gemv_f16_plan_info(out_dim: i32, in_dim: i32, rows: i32, tile_rows: *mut i32,
+                                   waves: *mut i32, blocks_per_wave: *mut i32, passes: *mut i32,
+                                   lds_bytes: *mut usize) -> c_int;
     pub fn ffai_gemv_f16_qkv_cache(w: *const c_void, bias: *const f32, in_dim: i32,
                                    x: *const f32, rows: i32, x_row_stride: i64, q: *mut f32,
                                    q_row_stride: i64, c: *const ffai_kv_cache,

@@ -69,3 +69,88 @@ def test_gemv_f16(gpu, out_dim, in_dim, rows):
     assert (np.abs(got - exact) <= bound).all()
     f32w = x.astype(np.float64) @ w.astype(np.float64).T  # f16_gemv.rs:203-229's bound
     assert np.abs(got - f32w).max() / np.abs(f32w).max() < 5e-3
+
+
+def _check_f16(got, w16, x):
+    exact = og.gemv_f16_exact(w16, x)
+    bound = 1e-5 * (np.abs(x.astype(np.float64)) @ np.abs(w16.astype(np.float64)).T)
+    assert (np.abs(got.astype(np.float64) - exact) <= bound).all()
+
+
+@pytest.mark.parametrize("rows", list(range(1, 17)))
+def test_gemv_f16_every_beam_count(gpu, rows):
+    """Every tile height the launch picks (1..16 rows per tile), ragged dimensions: out_dim not a
+    multiple of the tile, in_dim not a multiple of a wave's 32-element blocks."""
+    rng = np.random.default_rng(80 + rows)
+    for out_dim, in_dim in ((1000, 1032), (77, 40), (300, 8)):
+        w16 = rng.standard_normal((out_dim, in_dim)).astype(np.float16)
+        x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+        got = F16Gemv(torch.from_numpy(w16).to(gpu))(torch.from_numpy(x).to(gpu)).cpu().numpy()
+        _check_f16(got, w16, x)
+
+
+def test_gemv_f16_wide_range_and_subnormal_weights(gpu):
+    """x is carried as a power-of-two scale and two f16 halves per (beam, range of elements):
+    beams whose magnitudes sit near f32's extremes, a range holding 1e-3 beside 1e4, and f16
+    subnormal weights keep the f32 summation bound."""
+    rng = np.random.default_rng(90)
+    out_dim, in_dim, rows = 1024, 4096, 6
+    w = rng.standard_normal((out_dim, in_dim)).astype(np.float32)
+    w[:, ::7] *= 1e-6  # f16 subnormals (below 6.1e-5)
+    w[:8] *= 1e-6      # rows of subnormals only: a flushed product would zero their sums
+    w16 = w.astype(np.float16)
+    assert (np.abs(w16[:, ::7]) < 6.1e-5).mean() > 0.9 and (np.abs(w16[:8]) < 6.1e-5).all()
+    x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+    x[1] *= 1e30
+    x[2] *= 1e-30
+    x[3, ::64] *= 1e4
+    x[4] = 0.0
+    x[5, 100:200] *= 1e-3
+    got = F16Gemv(torch.from_numpy(w16).to(gpu))(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    assert np.isfinite(got).all()
+    _check_f16(got, w16, x)
+    assert (got[4] == 0).all()
+
+
+def test_gemv_f16_infinite_input(gpu):
+    """An infinite activation gives the infinite sums f32 arithmetic gives (its low half is 0),
+    and leaves the other beams untouched."""
+    rng = np.random.default_rng(91)
+    out_dim, in_dim = 512, 1024
+    w16 = rng.standard_normal((out_dim, in_dim)).astype(np.float16)
+    w16[w16 == 0] = 1
+    x = rng.standard_normal((3, in_dim)).astype(np.float32)
+    x[1, 37] = np.inf
+    got = F16Gemv(torch.from_numpy(w16).to(gpu))(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = np.where(w16[:, 37].astype(np.float32) > 0, np.inf, -np.inf)
+    np.testing.assert_array_equal(got[1], want)
+    _check_f16(got[[0, 2]], w16, x[[0, 2]])
+
+
+def test_gemv_f16_repeatable(gpu):
+    """The waves' partial tiles are summed in a fixed order: two calls give the same bits."""
+    rng = np.random.default_rng(92)
+    w = torch.from_numpy(rng.standard_normal((4096, 1024)).astype(np.float32)).to(gpu)
+    g = F16Gemv(w)
+    x = torch.from_numpy(rng.standard_normal((5, 1024)).astype(np.float32)).to(gpu)
+    a = g(x)
+    b = g(x)
+    assert torch.equal(a, b)
+
+
+# (out_dim, in_dim, rows) selecting each compile-time specialized launch shape of gemv.hip
+# (tile rows, waves, blocks per wave, x loads), beside shapes that take the generic kernel
+SPECIALIZED = [(1024, 1024, 5), (1024, 1024, 6), (1024, 1024, 7), (1024, 1024, 8),
+               (4096, 1024, 1), (3072, 1024, 4), (4096, 1024, 5), (3072, 1024, 8),
+               (4096, 1024, 9), (4096, 1024, 16), (1024, 4096, 5), (1024, 4096, 6),
+               (1024, 4096, 8), (1024, 1024, 1), (1024, 4096, 1), (1280, 1280, 5),
+               (1280, 1280, 6), (3840, 1280, 5), (5120, 1280, 6), (1280, 5120, 5)]
+
+
+@pytest.mark.parametrize("out_dim,in_dim,rows", SPECIALIZED)
+def test_gemv_f16_launch_shapes(gpu, out_dim, in_dim, rows):
+    rng = np.random.default_rng(out_dim + 3 * in_dim + rows)
+    w16 = rng.standard_normal((out_dim, in_dim)).astype(np.float16)
+    x = rng.standard_normal((rows, in_dim)).astype(np.float32)
+    got = F16Gemv(torch.from_numpy(w16).to(gpu))(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    _check_f16(got, w16, x)
