@@ -402,10 +402,22 @@ __global__ __launch_bounds__(256) void vocab_act_quant_kernel(const float* __res
   if (item_id() == 0) sx_out[r] = sx;
 }
 
-// Workgroup: kVocabRowsPerWg vocabulary rows (4 per wave). Phase 1: lane l takes 16-byte chunks
-// l, l + 64, ... of a row, four v_dot4 per chunk and beam, and adds the exact partial into its
-// block's sum in LDS. Phase 2: one thread per (beam, row) runs the in-order float sum over blocks.
+// Workgroup: kVocabRowsPerWg = 16 vocabulary rows. Phase 1 on the matrix cores
+// (v_mfma_i32_16x16x64_i8, exact integer products and sums): the 16 rows are the A operand, lane
+// l holding bytes 16 (l / 16) .. +15 of row l % 16 in each 64-element step. The B columns are
+// (beam b, half h) = b % 8 + 8 h: beam b's activations over the step's half h (32 elements, which
+// lie inside one block since blocks are multiples of 32) and zero over the other half, so
+// C[row][b % 8 + 8 h] is that half's exact dot, added into its block's sum in LDS (stored
+// directly when blocks are 32 elements, each sum then having one contribution). Beams 8-15 take a
+// second product. Each wave takes every fourth step, a batch of steps per round trip, the
+// activations loaded before the weights: beside a one-row-per-wave dot loop this reads each
+// activation once per 16 rows instead of once per row, and needs no LDS atomics. Phase 2: one
+// thread per (beam, row) runs the in-order float sum over blocks.
 constexpr int kVocabRowsPerWg = 16;
+constexpr int kVocabSteps = 4;  // 64-element steps per wave and round trip
+constexpr int kVocabScPerLane = 4;  // block scales per lane: 16 rows x up to 64 blocks
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void vocab_logits_kernel(
     const int8_t* __restrict__ qw, const float* __restrict__ bscale,
@@ -413,29 +425,81 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
     const int8_t* __restrict__ xu, int d_pad, const float* __restrict__ sx,
     float* __restrict__ logits, int64_t ls) {
 #pragma clang fp contract(off)  // separately rounded multiply and add, as in the reference
-  extern __shared__ int bs_lds[];  // [rows][kVocabRowsPerWg][nb]
+  extern __shared__ int bs_lds[];  // [rows][kVocabRowsPerWg][nb] block sums, then the scales
   const int nb = d / blk;
   const int v0 = wg_id_x() * kVocabRowsPerWg;
-  const int n_bs = rows * kVocabRowsPerWg * nb;
-  for (int i = item_id(); i < n_bs; i += 256) bs_lds[i] = 0;
-  __syncthreads();
-  const int wave = item_id() >> 6, lane = item_id() & 63;
-  const int chunks = d / 16;
-  for (int j = 0; j < kVocabRowsPerWg / 4; ++j) {
-    const int rl = wave * (kVocabRowsPerWg / 4) + j;  // row within the workgroup
-    const int v = v0 + rl;
-    if (v >= vocab) break;
-    for (int c = lane; c < chunks; c += 64) {
-      const u32x4 wv = *reinterpret_cast<const u32x4*>(qw + (int64_t)v * d + 16 * c);
-      const int b = (16 * c) / blk;
-      for (int r = 0; r < rows; ++r) {
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(xu + (int64_t)r * d_pad + 16 * c);
-        int s = 0;
+  float* sc_lds = reinterpret_cast<float*>(bs_lds + rows * kVocabRowsPerWg * nb);
+  const bool single = blk == 32;  // one contribution per block sum: stores, no zeroing
+  // the workgroup's block scales (kVocabRowsPerWg * nb contiguous floats), loaded before the
+  // operands so that they land with them; to LDS after the products
+  const int n_sc = min(kVocabRowsPerWg, vocab - v0) * nb;
+  const bool sc_staged = kVocabRowsPerWg * nb <= 256 * kVocabScPerLane;  // else read in phase 2
+  float scv[kVocabScPerLane];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_sdot4((int)xv[e], (int)wv[e], s, false);
-        atomicAdd(&bs_lds[(r * kVocabRowsPerWg + rl) * nb + b], s);
+  for (int i = 0; i < kVocabScPerLane; ++i)
+    scv[i] = bscale[(int64_t)v0 * nb + min(item_id() + 256 * i, n_sc - 1)];
+  if (!single) {
+    const int n_bs = rows * kVocabRowsPerWg * nb;
+    for (int i = item_id(); i < n_bs; i += 256) bs_lds[i] = 0;
+    __syncthreads();
+  }
+  auto phase1 = [&](auto ngroups) {
+    constexpr int NG = decltype(ngroups)::value;  // product groups of 8 beams
+    const int wave = item_id() >> 6, lane = item_id() & 63;
+    const int m = lane & 15, g = lane >> 4;
+    const int steps = (d + 63) / 64;
+    const int8_t* arow = qw + (int64_t)min(v0 + m, vocab - 1) * d;
+    for (int s0 = wave; s0 < steps; s0 += 4 * kVocabSteps) {
+      // activations first, then the weights; every address clamped to valid data, inactive
+      // operands zeroed afterwards (a load on one side of a branch would make the compiler wait
+      // for all loads at the join)
+      u32x4 bx[NG][kVocabSteps], av[kVocabSteps];
+#pragma unroll
+      for (int gr = 0; gr < NG; ++gr)
+#pragma unroll
+        for (int j = 0; j < kVocabSteps; ++j) {
+          const int bb = min((m & 7) + 8 * gr, rows - 1);
+          const int k = min(64 * (s0 + 4 * j) + 16 * g, d - 16);
+          bx[gr][j] = *reinterpret_cast<const u32x4*>(xu + (int64_t)bb * d_pad + k);
+        }
+#pragma unroll
+      for (int j = 0; j < kVocabSteps; ++j)
+        av[j] = *reinterpret_cast<const u32x4*>(arow + min(64 * (s0 + 4 * j) + 16 * g, d - 16));
+#pragma unroll
+      for (int j = 0; j < kVocabSteps; ++j) {
+        const int st = s0 + 4 * j;
+        if (st >= steps) break;  // wave-uniform
+#pragma unroll
+        for (int gr = 0; gr < NG; ++gr) {
+          const int b = (m & 7) + 8 * gr, h = m >> 3;
+          const bool on = b < rows && (g >> 1) == h && 64 * st + 16 * g < d;
+          u32x4 bv;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[e] = on ? bx[gr][j][e] : 0u;
+          const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              __builtin_bit_cast(i32x4, av[j]), __builtin_bit_cast(i32x4, bv),
+              i32x4{0, 0, 0, 0}, 0, 0, 0);
+          // D lane l holds rows 4 (l / 16) .. +3 of column l % 16 = m: beam b, half h
+          const int k0 = 64 * st + 32 * h;
+          if (b < rows && k0 < d) {
+            const int blkx = k0 / blk;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              int* dst = &bs_lds[(b * kVocabRowsPerWg + 4 * g + i) * nb + blkx];
+              if (single) *dst = c[i];
+              else atomicAdd(dst, c[i]);
+            }
+          }
+        }
       }
     }
+  };
+  if (rows <= 8) phase1(std::integral_constant<int, 1>{});
+  else phase1(std::integral_constant<int, 2>{});
+  if (sc_staged) {
+#pragma unroll
+    for (int i = 0; i < kVocabScPerLane; ++i)
+      if (item_id() + 256 * i < n_sc) sc_lds[item_id() + 256 * i] = scv[i];
   }
   __syncthreads();
   for (int t = item_id(); t < rows * kVocabRowsPerWg; t += 256) {
@@ -443,8 +507,9 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
     const int v = v0 + rl;
     if (v >= vocab) continue;
     const int* bsr = bs_lds + (r * kVocabRowsPerWg + rl) * nb;
-    const float* scr = bscale + (int64_t)v * nb;
+    const float* scr = sc_staged ? sc_lds + rl * nb : bscale + (int64_t)v * nb;
     float acc = 0.f;
+#pragma unroll 8
     for (int b = 0; b < nb; ++b) acc = acc + (float)bsr[b] * scr[b];
     logits[r * ls + v] = (acc - corr[v]) * sx[r];
   }
@@ -459,7 +524,10 @@ namespace {
 constexpr int kMaxGemvRows = 16;
 size_t pad16(size_t n) { return (n + 15) & ~size_t(15); }
 size_t vocab_lds_bytes(int d, int blk, int rows) {
-  return (size_t)rows * kVocabRowsPerWg * (d / blk) * sizeof(int);
+  // block sums of every (beam, row, block), then the rows' block scales when they are staged
+  const int nb = d / blk;
+  const int staged = kVocabRowsPerWg * nb <= 256 * kVocabScPerLane ? 1 : 0;
+  return (size_t)(rows + staged) * kVocabRowsPerWg * nb * sizeof(int);
 }
 constexpr size_t kVocabLdsMax = 48 * 1024;
 }  // namespace

@@ -54,6 +54,24 @@ def test_vocab_logits_bit_exact(gpu, d, rows, vocab):
     np.testing.assert_array_equal(got.argmax(axis=1), want.argmax(axis=1))
 
 
+@pytest.mark.parametrize("d,rows,vocab,blk", [(416, 3, 1000, 32), (384, 7, 2000, 64),
+                                              (1024, 12, 3000, 128), (1280, 9, 517, 32),
+                                              (96, 1, 33, 32), (4096, 3, 700, 32)])
+def test_vocab_logits_blocks_and_ragged_steps(gpu, d, rows, vocab, blk):
+    """Block sizes 32/64/128 (the products' 32-element halves stored or added per block), d with
+    a trailing half step (416 = 6.5 x 64), 9-12 beams (a second product for beams 8-15), a
+    vocabulary that ends inside a workgroup, and 128 blocks per row (scales read from global
+    memory instead of LDS): logits equal the oracle's bit for bit."""
+    rng = np.random.default_rng(73 + d + blk)
+    emb = (rng.standard_normal((vocab, d)) / np.sqrt(d)).astype(np.float32)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    iv = Int8Vocab(torch.from_numpy(emb).to(gpu), blk)
+    got = iv(torch.from_numpy(x).to(gpu)).cpu().numpy()
+    q, sc, corr = og.vocab_quantize(emb, blk)
+    want = og.vocab_logits(q, sc, corr, x, blk)
+    np.testing.assert_array_equal(got, want)
+
+
 @pytest.mark.parametrize("out_dim,in_dim,rows", [(1536, 384, 1), (1024, 1024, 5),
                                                  (4096, 1024, 5), (1024, 4096, 9), (1023, 1280, 16),
                                                  (3840, 1280, 5)])
