@@ -409,16 +409,20 @@ __global__ __launch_bounds__(256) void vocab_act_quant_kernel(const float* __res
 // lie inside one block since blocks are multiples of 32) and zero over the other half, so
 // C[row][b % 8 + 8 h] is that half's exact dot, added into its block's sum in LDS (stored
 // directly when blocks are 32 elements, each sum then having one contribution). Beams 8-15 take a
-// second product. Each wave takes every fourth step, a batch of steps per round trip, the
-// activations loaded before the weights: beside a one-row-per-wave dot loop this reads each
-// activation once per 16 rows instead of once per row, and needs no LDS atomics. Phase 2: one
-// thread per (beam, row) runs the in-order float sum over blocks.
+// second product (a second instance, NG = 2, so that up to 8 beams keep the registers of one).
+// Each wave takes four consecutive steps per round trip, the activations loaded before the
+// weights: beside a one-row-per-wave dot loop this reads each activation once per 16 rows
+// instead of once per row, and needs no LDS atomics. Phase 2: one thread per (beam, row) runs
+// the in-order float sum over blocks, then the workgroup ends; this serial tail, not the load
+// pattern (consecutive or interleaved steps) or the occupancy (4 or 7 waves per SIMD), bounds
+// the kernel at ~2.1 TB/s.
 constexpr int kVocabRowsPerWg = 16;
 constexpr int kVocabSteps = 4;  // 64-element steps per wave and round trip
 constexpr int kVocabScPerLane = 4;  // block scales per lane: 16 rows x up to 64 blocks
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+template <int NG>  // products per step: groups of 8 beams (1 for rows <= 8, else 2)
 __global__ __launch_bounds__(256) void vocab_logits_kernel(
     const int8_t* __restrict__ qw, const float* __restrict__ bscale,
     const float* __restrict__ corr, int vocab, int d, int blk, int rows,
@@ -443,13 +447,12 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
     for (int i = item_id(); i < n_bs; i += 256) bs_lds[i] = 0;
     __syncthreads();
   }
-  auto phase1 = [&](auto ngroups) {
-    constexpr int NG = decltype(ngroups)::value;  // product groups of 8 beams
+  {
     const int wave = item_id() >> 6, lane = item_id() & 63;
     const int m = lane & 15, g = lane >> 4;
     const int steps = (d + 63) / 64;
     const int8_t* arow = qw + (int64_t)min(v0 + m, vocab - 1) * d;
-    for (int s0 = wave; s0 < steps; s0 += 4 * kVocabSteps) {
+    for (int s0 = wave * kVocabSteps; s0 < steps; s0 += 4 * kVocabSteps) {
       // activations first, then the weights; every address clamped to valid data, inactive
       // operands zeroed afterwards (a load on one side of a branch would make the compiler wait
       // for all loads at the join)
@@ -459,15 +462,15 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
 #pragma unroll
         for (int j = 0; j < kVocabSteps; ++j) {
           const int bb = min((m & 7) + 8 * gr, rows - 1);
-          const int k = min(64 * (s0 + 4 * j) + 16 * g, d - 16);
+          const int k = min(64 * (s0 + j) + 16 * g, d - 16);
           bx[gr][j] = *reinterpret_cast<const u32x4*>(xu + (int64_t)bb * d_pad + k);
         }
 #pragma unroll
       for (int j = 0; j < kVocabSteps; ++j)
-        av[j] = *reinterpret_cast<const u32x4*>(arow + min(64 * (s0 + 4 * j) + 16 * g, d - 16));
+        av[j] = *reinterpret_cast<const u32x4*>(arow + min(64 * (s0 + j) + 16 * g, d - 16));
 #pragma unroll
       for (int j = 0; j < kVocabSteps; ++j) {
-        const int st = s0 + 4 * j;
+        const int st = s0 + j;
         if (st >= steps) break;  // wave-uniform
 #pragma unroll
         for (int gr = 0; gr < NG; ++gr) {
@@ -493,9 +496,8 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
         }
       }
     }
-  };
-  if (rows <= 8) phase1(std::integral_constant<int, 1>{});
-  else phase1(std::integral_constant<int, 2>{});
+  }
+
   if (sc_staged) {
 #pragma unroll
     for (int i = 0; i < kVocabScPerLane; ++i)
@@ -680,8 +682,14 @@ int ffai_vocab_int8_logits(const int8_t* qw, const float* bscale, const float* c
   hipLaunchKernelGGL(vocab_act_quant_kernel, dim3(rows), dim3(256), 0, st, x, x_row_stride, d, d_pad,
                      xu, sx);
   const dim3 grid((unsigned)((vocab + kVocabRowsPerWg - 1) / kVocabRowsPerWg));
-  hipLaunchKernelGGL(vocab_logits_kernel, grid, dim3(256), vocab_lds_bytes(d, blk, rows), st, qw,
-                     bscale, corr, vocab, d, blk, rows, xu, d_pad, sx, logits, logits_row_stride);
+  if (rows <= 8)
+    hipLaunchKernelGGL(vocab_logits_kernel<1>, grid, dim3(256), vocab_lds_bytes(d, blk, rows), st,
+                       qw, bscale, corr, vocab, d, blk, rows, xu, d_pad, sx, logits,
+                       logits_row_stride);
+  else
+    hipLaunchKernelGGL(vocab_logits_kernel<2>, grid, dim3(256), vocab_lds_bytes(d, blk, rows), st,
+                       qw, bscale, corr, vocab, d, blk, rows, xu, d_pad, sx, logits,
+                       logits_row_stride);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return api_fail(FFAI_ERR_HIP, hipGetErrorString(e));
   return FFAI_OK;
