@@ -266,11 +266,12 @@ GemvShape gemv_shape(int out_dim, int in_dim, int rows) {
   return s;
 }
 
-// One kernel instance on its launch shape; dynamic LDS above 64 KB is allowed once per instance
-// (up to the CU's 160 KB).
-template <typename K>
-hipError_t launch_one(K kern, size_t lds, dim3 grid, dim3 block, hipStream_t st,
-                      const GemvParams& p, const QkvCacheParams& qp) {
+// One kernel instance on its launch shape. Dynamic LDS above 64 KB is allowed once per instance
+// (up to the CU's 160 KB): the static lives in the instance's own function.
+template <int NJ, int EPI, int CDT, int TL = -1, int NW = 0, int NXL = 0>
+hipError_t launch_one(size_t lds, dim3 grid, dim3 block, hipStream_t st, const GemvParams& p,
+                      const QkvCacheParams& qp) {
+  auto kern = gemv_f16_kernel<NJ, EPI, CDT, TL, NW, NXL>;
   if (lds > 65536) {
     static const hipError_t allowed = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -286,8 +287,7 @@ template <int EPI, int CDT, int TL, int NW, int NJ, int NXL>
 bool try_spec(const GemvShape& s, int nxl, dim3 grid, hipStream_t st, const GemvParams& p,
               const QkvCacheParams& qp, hipError_t& e) {
   if (s.tr_log2 != TL || s.nw != NW || s.nj != NJ || s.passes != 1 || nxl > NXL) return false;
-  e = launch_one(gemv_f16_kernel<NJ, EPI, CDT, TL, NW, NXL>, s.lds, grid, dim3(64 * NW), st, p,
-                 qp);
+  e = launch_one<NJ, EPI, CDT, TL, NW, NXL>(s.lds, grid, dim3(64 * NW), st, p, qp);
   return true;
 }
 
@@ -324,9 +324,9 @@ hipError_t launch_gemv(GemvParams p, const QkvCacheParams& qp, int out_rows, hip
       return e;
   }
   const dim3 block(64 * s.nw);
-  if (s.nj == 1) return launch_one(gemv_f16_kernel<1, EPI, CDT>, s.lds, grid, block, st, p, qp);
-  if (s.nj == 2) return launch_one(gemv_f16_kernel<2, EPI, CDT>, s.lds, grid, block, st, p, qp);
-  return launch_one(gemv_f16_kernel<4, EPI, CDT>, s.lds, grid, block, st, p, qp);
+  if (s.nj == 1) return launch_one<1, EPI, CDT>(s.lds, grid, block, st, p, qp);
+  if (s.nj == 2) return launch_one<2, EPI, CDT>(s.lds, grid, block, st, p, qp);
+  return launch_one<4, EPI, CDT>(s.lds, grid, block, st, p, qp);
 }
 
 // ---- int8 vocabulary projection -------------------------------------------------------------
