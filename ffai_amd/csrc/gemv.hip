@@ -414,9 +414,9 @@ __global__ __launch_bounds__(256) void vocab_act_quant_kernel(const float* __res
 // weights: beside a one-row-per-wave dot loop this reads each activation once per 16 rows
 // instead of once per row, and needs no LDS atomics. Phase 2: one thread per (beam, row) runs
 // the in-order float sum over blocks, then the workgroup ends. The kernel streams ~2.1 TB/s;
-// neither the load order (consecutive or interleaved steps) nor the occupancy (4 or 7 waves per
-// SIMD) changed that, which leaves each 16-row workgroup's fixed chain (operands, products,
-// barrier, serial float tail) around its 16 KB of weights as the suspect.
+// neither the load order (consecutive or interleaved steps), the occupancy (4 or 7 waves per
+// SIMD) nor 32 rows per workgroup (29.5 us) changed that. The weights' operand layout reads 64
+// bytes of each of 16 rows per load instruction, half of each 128-byte line.
 constexpr int kVocabRowsPerWg = 16;
 constexpr int kVocabSteps = 4;  // 64-element steps per wave and round trip
 constexpr int kVocabScPerLane = 4;  // block scales per lane: 16 rows x up to 64 blocks
