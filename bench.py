@@ -1009,10 +1009,36 @@ def gemv_bench(torch, steps, warmup, beams=5, n=1024, layers=24, vocab=51865):
     e1.record()
     torch.cuda.synchronize()
     us_vocab = e0.elapsed_time(e1) * 1e3 / steps
+    # per shape: graphs of 24 dependent launches over distinct weights, two sets alternating so
+    # that the weights replayed (2 x 24 matrices) exceed the 256 MB MALL for the larger shapes
+    per_launch = {}
+    for o, i in dict.fromkeys(shapes):  # the distinct shapes, in order
+        si = shapes.index((o, i))
+        extra = [F16Gemv(torch.randn(o, i, generator=g, device=dev) / i ** 0.5)
+                 for _ in range(layers)]
+        sets = [[layer[si] for layer in mats], extra]
+        graphs = []
+        for ms in sets:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for m in ms:
+                    m(xs[i], out=ys[o])
+            graphs.append(gr)
+        for k in range(4):
+            graphs[k % 2].replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for k in range(2 * steps):
+            graphs[k % 2].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per_launch[f"{o}x{i}"] = e0.elapsed_time(e1) * 1e3 / (2 * steps) / layers
+        del graphs, extra
     return {"us_per_step": us, "bytes_per_step": f16_bytes + vocab_bytes,
             "gbps": (f16_bytes + vocab_bytes) / (us * 1e-6) / 1e9,
             "vocab_us": us_vocab, "vocab_gbps": vocab_bytes / (us_vocab * 1e-6) / 1e9,
-            "launches_per_step": layers * len(shapes) + 2, "beams": beams}
+            "launches_per_step": layers * len(shapes) + 2, "beams": beams,
+            "us_per_launch": per_launch}
 
 
 # ------------------------------------------------------------------------------------------
@@ -1235,7 +1261,8 @@ def main():
         log("decoder GEMVs: beam-5 whisper-medium step ...")
         gv = gemv_bench(torch, 50, 5)
         log(f"decoder GEMVs: {gv['us_per_step']:.1f} us/step ({gv['gbps']:.0f} GB/s); vocabulary "
-            f"projection {gv['vocab_us']:.1f} us ({gv['vocab_gbps']:.0f} GB/s)")
+            f"projection {gv['vocab_us']:.1f} us ({gv['vocab_gbps']:.0f} GB/s); per launch "
+            + ", ".join(f"{k} {v:.2f} us" for k, v in gv["us_per_launch"].items()))
         extras["decoder_gemv_beam5"] = gv
     if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")
