@@ -413,10 +413,9 @@ __global__ __launch_bounds__(256) void vocab_act_quant_kernel(const float* __res
 // Each wave takes four consecutive steps per round trip, the activations loaded before the
 // weights: beside a one-row-per-wave dot loop this reads each activation once per 16 rows
 // instead of once per row, and needs no LDS atomics. Phase 2: one thread per (beam, row) runs
-// the in-order float sum over blocks, then the workgroup ends. The kernel streams ~2.1 TB/s;
-// neither the load order (consecutive or interleaved steps), the occupancy (4 or 7 waves per
-// SIMD) nor 32 rows per workgroup (29.5 us) changed that. The weights' operand layout reads 64
-// bytes of each of 16 rows per load instruction, half of each 128-byte line.
+// the in-order float sum over blocks (LDS rows of nb + 1 words: at nb words the 64 lanes of
+// each of its reads fell in two banks, and that phase cost as much as streaming the weights),
+// then the workgroup ends.
 constexpr int kVocabRowsPerWg = 16;
 constexpr int kVocabSteps = 4;  // 64-element steps per wave and round trip
 constexpr int kVocabScPerLane = 4;  // block scales per lane: 16 rows x up to 64 blocks
@@ -430,10 +429,12 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
     const int8_t* __restrict__ xu, int d_pad, const float* __restrict__ sx,
     float* __restrict__ logits, int64_t ls) {
 #pragma clang fp contract(off)  // separately rounded multiply and add, as in the reference
-  extern __shared__ int bs_lds[];  // [rows][kVocabRowsPerWg][nb] block sums, then the scales
-  const int nb = d / blk;
+  // [rows][kVocabRowsPerWg][nb] block sums, then the rows' scales, rows of nb + 1 words: phase 2
+  // walks a row per thread, and an even stride put all 64 lanes of a read in two banks
+  extern __shared__ int bs_lds[];
+  const int nb = d / blk, nbs = nb + 1;
   const int v0 = wg_id_x() * kVocabRowsPerWg;
-  float* sc_lds = reinterpret_cast<float*>(bs_lds + rows * kVocabRowsPerWg * nb);
+  float* sc_lds = reinterpret_cast<float*>(bs_lds + rows * kVocabRowsPerWg * nbs);
   const bool single = blk == 32;  // one contribution per block sum: stores, no zeroing
   // the workgroup's block scales (kVocabRowsPerWg * nb contiguous floats), loaded before the
   // operands so that they land with them; to LDS after the products
@@ -444,7 +445,7 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
   for (int i = 0; i < kVocabScPerLane; ++i)
     scv[i] = bscale[(int64_t)v0 * nb + min(item_id() + 256 * i, n_sc - 1)];
   if (!single) {
-    const int n_bs = rows * kVocabRowsPerWg * nb;
+    const int n_bs = rows * kVocabRowsPerWg * nbs;
     for (int i = item_id(); i < n_bs; i += 256) bs_lds[i] = 0;
     __syncthreads();
   }
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
             const int blkx = k0 / blk;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              int* dst = &bs_lds[(b * kVocabRowsPerWg + 4 * g + i) * nb + blkx];
+              int* dst = &bs_lds[(b * kVocabRowsPerWg + 4 * g + i) * nbs + blkx];
               if (single) *dst = c[i];
               else atomicAdd(dst, c[i]);
             }
@@ -501,16 +502,18 @@ __global__ __launch_bounds__(256) void vocab_logits_kernel(
 
   if (sc_staged) {
 #pragma unroll
-    for (int i = 0; i < kVocabScPerLane; ++i)
-      if (item_id() + 256 * i < n_sc) sc_lds[item_id() + 256 * i] = scv[i];
+    for (int i = 0; i < kVocabScPerLane; ++i) {
+      const int idx = item_id() + 256 * i;  // scale idx of the workgroup's rows: row idx / nb
+      if (idx < n_sc) sc_lds[idx + idx / nb] = scv[i];
+    }
   }
   __syncthreads();
   for (int t = item_id(); t < rows * kVocabRowsPerWg; t += 256) {
     const int r = t / kVocabRowsPerWg, rl = t % kVocabRowsPerWg;
     const int v = v0 + rl;
     if (v >= vocab) continue;
-    const int* bsr = bs_lds + (r * kVocabRowsPerWg + rl) * nb;
-    const float* scr = sc_staged ? sc_lds + rl * nb : bscale + (int64_t)v * nb;
+    const int* bsr = bs_lds + (r * kVocabRowsPerWg + rl) * nbs;
+    const float* scr = sc_staged ? sc_lds + rl * nbs : bscale + (int64_t)v * nb;
     float acc = 0.f;
 #pragma unroll 8
     for (int b = 0; b < nb; ++b) acc = acc + (float)bsr[b] * scr[b];
@@ -530,9 +533,9 @@ size_t vocab_lds_bytes(int d, int blk, int rows) {
   // block sums of every (beam, row, block), then the rows' block scales when they are staged
   const int nb = d / blk;
   const int staged = kVocabRowsPerWg * nb <= 256 * kVocabScPerLane ? 1 : 0;
-  return (size_t)(rows + staged) * kVocabRowsPerWg * nb * sizeof(int);
+  return (size_t)(rows + staged) * kVocabRowsPerWg * (nb + 1) * sizeof(int);
 }
-constexpr size_t kVocabLdsMax = 48 * 1024;
+constexpr size_t kVocabLdsMax = 64 * 1024;
 }  // namespace
 
 extern "C" {
