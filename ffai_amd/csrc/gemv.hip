@@ -376,30 +376,25 @@ __global__ __launch_bounds__(256) void vocab_quantize_kernel(const store_t<DT>* 
 }
 
 // Per activation row: sx = amax / 63; x_u = round(x / sx) clamped to [-64, 63], plus 64 (0..127,
-// held as int8 for v_dot4). Workspace: rows * d bytes of x_u (16-byte aligned rows), then sx.
-__global__ __launch_bounds__(256) void vocab_act_quant_kernel(const float* __restrict__ x,
-                                                              int64_t xs, int d, int d_pad,
-                                                              int8_t* __restrict__ xu,
-                                                              float* __restrict__ sx_out) {
+// held as int8 for the integer products). Workspace: rows * d bytes of x_u (16-byte aligned
+// rows), then sx. One wave per row: the row max by DPP and lane swaps (a max is the same in any
+// order), no barrier.
+__global__ __launch_bounds__(64) void vocab_act_quant_kernel(const float* __restrict__ x,
+                                                             int64_t xs, int d, int d_pad,
+                                                             int8_t* __restrict__ xu,
+                                                             float* __restrict__ sx_out) {
 #pragma clang fp contract(off)
-  const int r = wg_id_x();
+  const int r = wg_id_x(), lane = item_id();
   const float* xr = x + r * xs;
-  __shared__ float red[256];
   float m = 0.f;
-  for (int k = item_id(); k < d; k += 256) m = fmaxf(m, fabsf(xr[k]));
-  red[item_id()] = m;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (item_id() < s) red[item_id()] = fmaxf(red[item_id()], red[item_id() + s]);
-    __syncthreads();
-  }
-  const float amax = red[0];
+  for (int k = lane; k < d; k += 64) m = fmaxf(m, fabsf(xr[k]));
+  const float amax = wave_max_all(m);
   const float sx = amax > 0.f ? __fdiv_rn(amax, 63.f) : 1.f;
-  for (int k = item_id(); k < d; k += 256) {
+  for (int k = lane; k < d; k += 64) {
     const float qf = fminf(fmaxf(round_away(__fdiv_rn(xr[k], sx)), -64.f), 63.f);
     xu[(int64_t)r * d_pad + k] = (int8_t)((int)qf + 64);
   }
-  if (item_id() == 0) sx_out[r] = sx;
+  if (lane == 0) sx_out[r] = sx;
 }
 
 // Workgroup: kVocabRowsPerWg = 16 vocabulary rows. Phase 1 on the matrix cores
@@ -683,7 +678,7 @@ int ffai_vocab_int8_logits(const int8_t* qw, const float* bscale, const float* c
   const int d_pad = (int)pad16(d);
   int8_t* xu = static_cast<int8_t*>(workspace);
   float* sx = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)rows * d_pad);
-  hipLaunchKernelGGL(vocab_act_quant_kernel, dim3(rows), dim3(256), 0, st, x, x_row_stride, d, d_pad,
+  hipLaunchKernelGGL(vocab_act_quant_kernel, dim3(rows), dim3(64), 0, st, x, x_row_stride, d, d_pad,
                      xu, sx);
   const dim3 grid((unsigned)((vocab + kVocabRowsPerWg - 1) / kVocabRowsPerWg));
   if (rows <= 8)
