@@ -200,8 +200,10 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
     // the next pass rewrites this region: its reads are done (one wave's LDS accesses complete
     // in order)
   }
-  // the waves' partial tiles, each in its own region: sum over parts and waves in a fixed order
-  reinterpret_cast<f32x4*>(xw)[lane] = acc;
+  // the waves' partial tiles, each in its own region: sum over parts and waves in a fixed order.
+  // Lane l's 4 floats at word 4 l + 16 (l / 16): the readers below take one value each, threads
+  // of a beam walking the tile rows, and unpadded those of a beam fell on the same 4 banks
+  reinterpret_cast<f32x4*>(xw + 2 * 16 * (lane >> 4))[lane] = acc;
   __syncthreads();
   for (int t = tid; t < (p.rows << tl); t += nw * 64) {
     const int b = t >> tl, rr = t & (tr - 1);  // beam b, tile row rr
@@ -215,8 +217,9 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
       float pv[16];
 #pragma unroll
       for (int ww = 0; ww < 16; ++ww)
-        pv[ww] = ww < nw ? reinterpret_cast<const float*>(gemv_lds + ww * (32 * RS))[4 * l + e]
-                           : 0.f;
+        pv[ww] = ww < nw ? reinterpret_cast<const float*>(
+                               gemv_lds + ww * (32 * RS))[4 * l + e + 16 * (l >> 4)]
+                         : 0.f;
 #pragma unroll
       for (int ww = 0; ww < 16; ++ww) v += pv[ww];
     }
