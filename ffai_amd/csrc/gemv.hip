@@ -78,7 +78,7 @@ struct QkvCacheParams {
   int32_t n, head_dim, capacity;
 };
 
-// Max over groups of G consecutive lanes (G = 8, 16 or 32; every lane gets its group's max).
+// Max over groups of G consecutive lanes (G = 8, 16, 32 or 64; every lane gets its group's max).
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
   v = fmaxf(v, dpp_mov<0xb1>(v));   // quad_perm [1,0,3,2]
@@ -90,17 +90,20 @@ __device__ __forceinline__ float group_max(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // lanes l and l ^ 16
     v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
   }
+  if constexpr (G >= 64) v = partner_max(v);  // lanes l and l ^ 32
   return v;
 }
 
 // EPI 0: y[b][o] = sum. EPI 1: the q/k/v epilogue, cache elements of type CDT.
 // TL >= 0: a specialized launch shape known at compile time (tile rows 1 << TL, NW waves, one
-// pass, the first NXL dense x loads hold every beam); the compiler then folds the index
-// arithmetic and unrolls the waves' reduction (~0.3-0.8 us per call at the decoder's shapes).
+// pass, the first NXL dense x loads hold every beam; ROWS > 0: exactly ROWS beams); the
+// compiler then folds the index arithmetic and unrolls the waves' reduction (~0.3-0.8 us per
+// call at the decoder's shapes).
 // TL < 0: the shape comes from the parameters.
-template <int NJ, int EPI, int CDT, int TL = -1, int NW = 0, int NXL = 0>
+template <int NJ, int EPI, int CDT, int TL = -1, int NW = 0, int NXL = 0, int ROWS = 0>
 __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCacheParams qp) {
   constexpr bool SPEC = TL >= 0;
+  const int rows = ROWS > 0 ? ROWS : p.rows;  // beams (x rows)
   constexpr int KW = 32 * NJ;  // elements of one part per wave and pass
   constexpr int RS = KW + 8;   // LDS row of a column (halves; 16 bytes of it hold the scale)
   constexpr int LPC = KW / 4;  // lanes per column in the dense x load
@@ -115,23 +118,35 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
   const int q = m >> tl, r = m & (tr - 1);  // A row m: weight row r of part q
   const int tile = wg_id_x();
   const uint16_t* wr = p.w + (int64_t)min(tile * tr + r, p.out_dim - 1) * p.in_dim;
-  uint16_t* xw = gemv_lds + wave * (32 * RS);  // this wave's hi rows [16][RS], then lo rows
-  const bool nv = (m & (tr - 1)) < p.rows;  // B column m holds a beam
-  const int ni = (qn * p.rows * LPC + 63) / 64;  // dense x loads that hold a beam
+  // this wave's LDS region: the hi rows of the columns that hold a beam (QN * rows of them,
+  // column (part, beam) at row part * rows + beam), then their lo rows; at least the 304 floats
+  // of the partial tile
+  const int ncol = qn * rows;
+  const int reg = max(2 * ncol * RS, 608);
+  uint16_t* xw = gemv_lds + wave * reg;
+  const bool nv = (m & (tr - 1)) < rows;  // B column m holds a beam
+  const int ncm = (m >> tl) * rows + (m & (tr - 1));  // and its LDS row when it does
+  const int ni = (ncol * LPC + 63) / 64;  // dense x loads that hold a beam
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int ps = 0; ps < (SPEC ? 1 : p.passes); ++ps) {
     const int kb = ps * qn * kp + wave * KW;
     // Dense x: load slot v = 0..15 is beam v / QN over part v % QN (column n = part TR + beam),
     // LPC lanes per slot, 4 elements each. Slots of beams >= rows load a valid beam's elements
     // and fill LDS rows that are never read; no branch, no division.
+    // (A generic instance with more than 8 loads takes the rest after the weights: all of them
+    // beside the weights would exceed the 128 registers of a 1024-lane workgroup.)
+    constexpr int NX1 = (SPEC || NI <= 8) ? NI : 4;
     f32x4 xv[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      if (SPEC && i >= NXL) break;
+    auto load_x = [&](int i) __attribute__((always_inline)) {
       const int f = 64 * i + lane, v = f / LPC;
-      const int b = min(v >> (4 - tl), p.rows - 1), part = v & (qn - 1);
+      const int b = min(v >> (4 - tl), rows - 1), part = v & (qn - 1);
       const int k = min(kb + part * kp + 4 * (f % LPC), p.in_dim - 4);
       xv[i] = *reinterpret_cast<const f32x4*>(p.x + b * p.xs + k);
+    };
+#pragma unroll
+    for (int i = 0; i < NX1; ++i) {
+      if (SPEC && i >= NXL) break;
+      load_x(i);
     }
     __builtin_amdgcn_sched_barrier(0);
     u32x4 a[NJ];
@@ -141,7 +156,11 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
     // split the loaded slots that hold a beam (the first QN * rows; the rest are never read)
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      if (SPEC ? i >= NXL : i >= ni) break;  // wave-uniform
+      if (SPEC ? i >= NXL : i >= ni) {  // wave-uniform
+        if constexpr (NX1 < NI) continue;  // (a loop of 16 with a load would not unroll on break)
+        else break;
+      }
+      if (i >= NX1) load_x(i);
       const int f = 64 * i + lane, v = f / LPC, c4 = f % LPC;
       const int b = v >> (4 - tl), part = v & (qn - 1);
       const bool ok = kb + part * kp + 4 * c4 < p.in_dim;
@@ -169,10 +188,12 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
                           ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16)
                     : 0u;
       }
-      const int n = (part << tl) + b;
-      *reinterpret_cast<u32x2*>(xw + n * RS + 4 * c4) = u32x2{hp[0], hp[1]};
-      *reinterpret_cast<u32x2*>(xw + (16 + n) * RS + 4 * c4) = u32x2{lp[0], lp[1]};
-      if (c4 == 0) xw[n * RS + KW] = (uint16_t)sb;
+      if (b < rows) {  // the last load's slots past the beams hold nothing to keep
+        const int n = part * rows + b;
+        *reinterpret_cast<u32x2*>(xw + n * RS + 4 * c4) = u32x2{hp[0], hp[1]};
+        *reinterpret_cast<u32x2*>(xw + (ncol + n) * RS + 4 * c4) = u32x2{lp[0], lp[1]};
+        if (c4 == 0) xw[n * RS + KW] = (uint16_t)sb;
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -182,8 +203,8 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
     for (int j = 0; j < NJ; ++j) {
       u32x4 bh = {0u, 0u, 0u, 0u}, bl = bh;
       if (nv) {
-        bh = ld16(xw + m * RS + 32 * j + 8 * g);
-        bl = ld16(xw + (16 + m) * RS + 32 * j + 8 * g);
+        bh = ld16(xw + ncm * RS + 32 * j + 8 * g);
+        bl = ld16(xw + (ncol + ncm) * RS + 32 * j + 8 * g);
       }
       const bool kin = kb + q * kp + 32 * j + 8 * g < p.in_dim;
       u32x4 aj;
@@ -193,7 +214,7 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
       c = mfma16x16<kF16>(aj, bl, c);
     }
     // D lane l holds rows 4 (l / 16) .. +3 of column l % 16 = m: the column's 1/s
-    const int sb = nv ? (int)xw[m * RS + KW] : 127;
+    const int sb = nv ? (int)xw[ncm * RS + KW] : 127;
     const float inv = __uint_as_float((uint32_t)(254 - sb) << 23);
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(c[e], inv, acc[e]);
@@ -205,7 +226,7 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
   // of a beam walking the tile rows, and unpadded those of a beam fell on the same 4 banks
   reinterpret_cast<f32x4*>(xw + 2 * 16 * (lane >> 4))[lane] = acc;
   __syncthreads();
-  for (int t = tid; t < (p.rows << tl); t += nw * 64) {
+  for (int t = tid; t < (rows << tl); t += nw * 64) {
     const int b = t >> tl, rr = t & (tr - 1);  // beam b, tile row rr
     const int o = tile * tr + rr;
     if (o >= p.out_dim) continue;
@@ -218,7 +239,7 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
 #pragma unroll
       for (int ww = 0; ww < 16; ++ww)
         pv[ww] = ww < nw ? reinterpret_cast<const float*>(
-                               gemv_lds + ww * (32 * RS))[4 * l + e + 16 * (l >> 4)]
+                               gemv_lds + ww * reg)[4 * l + e + 16 * (l >> 4)]
                          : 0.f;
 #pragma unroll
       for (int ww = 0; ww < 16; ++ww) v += pv[ww];
@@ -248,7 +269,8 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
 
 // Launch shape for (out_dim, in_dim, rows): the largest tile (<= 16 rows, >= rows) that still
 // gives ~192 workgroups, then per part the fewest passes with at most 16 waves, 32 NJ elements
-// each (NJ 2 or 4; 1 for a single block).
+// each (NJ 2, 4 or 8; 1 for a single block), NJ halved while the waves' LDS regions would exceed
+// the CU's 160 KB.
 struct GemvShape {
   int tr_log2, nw, nj, passes;
   size_t lds;
@@ -262,19 +284,26 @@ GemvShape gemv_shape(int out_dim, int in_dim, int rows) {
   const int bpp = (in_dim / 8 + 4 * qn - 1) / (4 * qn);  // 32-element blocks per part
   GemvShape s{};
   s.tr_log2 = tl;
-  s.nj = bpp == 1 ? 1 : (bpp + 1) / 2 <= 16 ? 2 : 4;
-  s.nw = std::min(16, (bpp + s.nj - 1) / s.nj);
-  s.passes = (bpp + s.nw * s.nj - 1) / (s.nw * s.nj);
-  s.lds = (size_t)s.nw * 64 * (32 * s.nj + 8);
+  s.nj = bpp == 1 ? 1 : (bpp + 1) / 2 <= 16 ? 2 : (bpp + 3) / 4 <= 16 ? 4 : 8;
+  for (;;) {
+    s.nw = std::min(16, (bpp + s.nj - 1) / s.nj);
+    s.passes = (bpp + s.nw * s.nj - 1) / (s.nw * s.nj);
+    // per wave: hi and lo rows (32 NJ + 8 halves) of the QN * rows columns holding a beam, at
+    // least the 304 floats of the partial tile
+    const size_t reg = std::max<size_t>((size_t)2 * qn * rows * (32 * s.nj + 8), 608);
+    s.lds = (size_t)s.nw * reg * 2;
+    if (s.lds <= 160 * 1024 || s.nj == 1) break;
+    s.nj /= 2;
+  }
   return s;
 }
 
 // One kernel instance on its launch shape. Dynamic LDS above 64 KB is allowed once per instance
 // (up to the CU's 160 KB): the static lives in the instance's own function.
-template <int NJ, int EPI, int CDT, int TL = -1, int NW = 0, int NXL = 0>
+template <int NJ, int EPI, int CDT, int TL = -1, int NW = 0, int NXL = 0, int ROWS = 0>
 hipError_t launch_one(size_t lds, dim3 grid, dim3 block, hipStream_t st, const GemvParams& p,
                       const QkvCacheParams& qp) {
-  auto kern = gemv_f16_kernel<NJ, EPI, CDT, TL, NW, NXL>;
+  auto kern = gemv_f16_kernel<NJ, EPI, CDT, TL, NW, NXL, ROWS>;
   if (lds > 65536) {
     static const hipError_t allowed = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -285,12 +314,14 @@ hipError_t launch_one(size_t lds, dim3 grid, dim3 block, hipStream_t st, const G
   return hipGetLastError();
 }
 
-// The specialized shape (TL, NW, NJ, NXL) if the call's shape is it and its beams fit NXL loads.
-template <int EPI, int CDT, int TL, int NW, int NJ, int NXL>
+// The specialized shape (TL, NW, NJ, NXL) if the call's shape is it and its beams fit NXL loads
+// (and number ROWS, if ROWS > 0).
+template <int EPI, int CDT, int TL, int NW, int NJ, int NXL, int ROWS = 0>
 bool try_spec(const GemvShape& s, int nxl, dim3 grid, hipStream_t st, const GemvParams& p,
               const QkvCacheParams& qp, hipError_t& e) {
   if (s.tr_log2 != TL || s.nw != NW || s.nj != NJ || s.passes != 1 || nxl > NXL) return false;
-  e = launch_one<NJ, EPI, CDT, TL, NW, NXL>(s.lds, grid, dim3(64 * NW), st, p, qp);
+  if (ROWS > 0 && p.rows != ROWS) return false;
+  e = launch_one<NJ, EPI, CDT, TL, NW, NXL, ROWS>(s.lds, grid, dim3(64 * NW), st, p, qp);
   return true;
 }
 
@@ -305,31 +336,35 @@ hipError_t launch_gemv(GemvParams p, const QkvCacheParams& qp, int out_rows, hip
   const int nxl = ((16 >> s.tr_log2) * p.rows * 8 * s.nj + 63) / 64;
   hipError_t e = hipSuccess;
   // the whisper decoders' projections, beam 5 and greedy: medium (d 1024: n x n, 3n x n, 4n x n,
-  // n x 4n) and large (d 1280)
+  // n x 4n) and large (d 1280, beam 5: n x n, 3n x n and 4n x n, n x 4n)
   if constexpr (EPI == 0) {
-    if (try_spec<EPI, CDT, 3, 8, 2, 3>(s, nxl, grid, st, p, qp, e) ||
+    if (try_spec<EPI, CDT, 3, 8, 2, 3, 5>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 3, 8, 2, 4>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 4, 16, 2, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 2, 5>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 4, 16, 2, 2>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 4, 16, 2, 4>(s, nxl, grid, st, p, qp, e) ||
-        try_spec<EPI, CDT, 3, 16, 4, 5>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 16, 4, 5, 5>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 3, 16, 4, 8>(s, nxl, grid, st, p, qp, e) ||
-        try_spec<EPI, CDT, 2, 4, 2, 1>(s, nxl, grid, st, p, qp, e) ||
-        try_spec<EPI, CDT, 2, 16, 2, 1>(s, nxl, grid, st, p, qp, e) ||
-        try_spec<EPI, CDT, 3, 10, 2, 3>(s, nxl, grid, st, p, qp, e) ||
-        try_spec<EPI, CDT, 4, 10, 4, 3>(s, nxl, grid, st, p, qp, e))
+        try_spec<EPI, CDT, 2, 4, 2, 1, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 2, 16, 2, 1, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 10, 2, 3, 5>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 10, 4, 3, 5>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 3, 10, 8, 10, 5>(s, nxl, grid, st, p, qp, e))
       return e;
   } else {
     if (try_spec<EPI, CDT, 4, 16, 2, 1>(s, nxl, grid, st, p, qp, e) ||
+        try_spec<EPI, CDT, 4, 16, 2, 2, 5>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 4, 16, 2, 2>(s, nxl, grid, st, p, qp, e) ||
         try_spec<EPI, CDT, 4, 16, 2, 4>(s, nxl, grid, st, p, qp, e) ||
-        try_spec<EPI, CDT, 4, 10, 4, 3>(s, nxl, grid, st, p, qp, e))
+        try_spec<EPI, CDT, 4, 10, 4, 3, 5>(s, nxl, grid, st, p, qp, e))
       return e;
   }
   const dim3 block(64 * s.nw);
   if (s.nj == 1) return launch_one<1, EPI, CDT>(s.lds, grid, block, st, p, qp);
   if (s.nj == 2) return launch_one<2, EPI, CDT>(s.lds, grid, block, st, p, qp);
-  return launch_one<4, EPI, CDT>(s.lds, grid, block, st, p, qp);
+  if (s.nj == 4) return launch_one<4, EPI, CDT>(s.lds, grid, block, st, p, qp);
+  return launch_one<8, EPI, CDT>(s.lds, grid, block, st, p, qp);
 }
 
 // ---- int8 vocabulary projection -------------------------------------------------------------
@@ -382,6 +417,10 @@ __global__ __launch_bounds__(256) void vocab_quantize_kernel(const store_t<DT>* 
 // held as int8 for the integer products). Workspace: rows * d bytes of x_u (16-byte aligned
 // rows), then sx. One wave per row: the row max by DPP and lane swaps (a max is the same in any
 // order), no barrier.
+// One wave per beam row. NC > 0 (d <= 256 NC, x rows 16-byte aligned): lane l holds elements
+// 4 l + 256 i .. +3 (i < NC) in registers, the row's loads issued together and read once. NC = 0:
+// a strided loop over the row.
+template <int NC>
 __global__ __launch_bounds__(64) void vocab_act_quant_kernel(const float* __restrict__ x,
                                                              int64_t xs, int d, int d_pad,
                                                              int8_t* __restrict__ xu,
@@ -389,13 +428,41 @@ __global__ __launch_bounds__(64) void vocab_act_quant_kernel(const float* __rest
 #pragma clang fp contract(off)
   const int r = wg_id_x(), lane = item_id();
   const float* xr = x + r * xs;
-  float m = 0.f;
-  for (int k = lane; k < d; k += 64) m = fmaxf(m, fabsf(xr[k]));
-  const float amax = wave_max_all(m);
-  const float sx = amax > 0.f ? __fdiv_rn(amax, 63.f) : 1.f;
-  for (int k = lane; k < d; k += 64) {
-    const float qf = fminf(fmaxf(round_away(__fdiv_rn(xr[k], sx)), -64.f), 63.f);
-    xu[(int64_t)r * d_pad + k] = (int8_t)((int)qf + 64);
+  int8_t* xq = xu + (int64_t)r * d_pad;
+  // q = round(x / sx) clamped to [-64, 63], stored offset by 64
+  auto quant = [](float v, float sx) __attribute__((always_inline)) {
+    return (int)fminf(fmaxf(round_away(__fdiv_rn(v, sx)), -64.f), 63.f) + 64;
+  };
+  float sx;
+  if constexpr (NC > 0) {
+    f32x4 v[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      v[i] = *reinterpret_cast<const f32x4*>(xr + min(4 * lane + 256 * i, d - 4));
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      if (4 * lane + 256 * i < d)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(v[i][e]));
+    const float amax = wave_max_all(m);
+    sx = amax > 0.f ? __fdiv_rn(amax, 63.f) : 1.f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int k = 4 * lane + 256 * i;
+      if (k < d) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) packed |= (uint32_t)quant(v[i][e], sx) << (8 * e);
+        *reinterpret_cast<uint32_t*>(xq + k) = packed;  // d_pad and the workspace: 16-byte aligned
+      }
+    }
+  } else {
+    float m = 0.f;
+    for (int k = lane; k < d; k += 64) m = fmaxf(m, fabsf(xr[k]));
+    const float amax = wave_max_all(m);
+    sx = amax > 0.f ? __fdiv_rn(amax, 63.f) : 1.f;
+    for (int k = lane; k < d; k += 64) xq[k] = (int8_t)quant(xr[k], sx);
   }
   if (lane == 0) sx_out[r] = sx;
 }
@@ -681,8 +748,14 @@ int ffai_vocab_int8_logits(const int8_t* qw, const float* bscale, const float* c
   const int d_pad = (int)pad16(d);
   int8_t* xu = static_cast<int8_t*>(workspace);
   float* sx = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)rows * d_pad);
-  hipLaunchKernelGGL(vocab_act_quant_kernel, dim3(rows), dim3(64), 0, st, x, x_row_stride, d, d_pad,
-                     xu, sx);
+  // d is a multiple of 32: whole 16-byte chunks when the rows are 16-byte aligned
+  const bool xa = (uintptr_t)x % 16 == 0 && (rows == 1 || x_row_stride % 4 == 0);
+  const int nc = xa ? (d + 255) / 256 : 0;
+  auto quant = nc == 0 ? vocab_act_quant_kernel<0>
+               : nc <= 2 ? vocab_act_quant_kernel<2>
+               : nc <= 4 ? vocab_act_quant_kernel<4>
+               : nc <= 8 ? vocab_act_quant_kernel<8> : vocab_act_quant_kernel<0>;
+  hipLaunchKernelGGL(quant, dim3(rows), dim3(64), 0, st, x, x_row_stride, d, d_pad, xu, sx);
   const dim3 grid((unsigned)((vocab + kVocabRowsPerWg - 1) / kVocabRowsPerWg));
   if (rows <= 8)
     hipLaunchKernelGGL(vocab_logits_kernel<1>, grid, dim3(256), vocab_lds_bytes(d, blk, rows), st,

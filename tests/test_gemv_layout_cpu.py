@@ -7,9 +7,10 @@ formulas are restated here and checked over a sweep of shapes:
   dynamic LDS the launch provides, and a workgroup fits a CU (<= 1024 lanes, <= 160 KB LDS);
 * every weight element of a row meets the same element of each beam's x exactly once: the
   MFMA contraction index (pass, part, wave, block, lane group, element) enumerates [0, in_dim)
-  once, the dense x load writes each (column, element) of the wave's LDS rows from the x element
-  the B read expects there, and the reduction reads C[q TR + r][q TR + b] from the lane and
-  register where the 16x16 D layout holds it;
+  once, the dense x load writes each (column, element) of the wave's LDS rows (QN * rows of
+  them, column (part, beam) at row part * rows + beam) from the x element the B read of MFMA
+  column part TR + beam expects there, and the reduction reads C[q TR + r][q TR + b] from the
+  lane and register where the 16x16 D layout holds it;
 * a numpy emulation of the whole tiling, the scaled hi/lo split of x included, equals the exact
   float64 product to the f32 summation bound the GPU test uses.
 """
@@ -26,14 +27,18 @@ SHAPES = [
     (1280, 1280, 5), (3840, 1280, 5), (5120, 1280, 5), (1280, 5120, 5),  # whisper-large beam 5
     (1024, 4096, 9), (1536, 384, 1), (1023, 1280, 16), (384, 384, 1), (1024, 1024, 1),
     (51, 40, 3), (7, 8, 1), (100, 5120, 2), (4096, 4096, 16), (17, 8200, 7), (33, 264, 4),
+    (1280, 8192, 5), (64, 20000, 16), (1024, 2560, 3), (1280, 6144, 5), (1024, 20000, 9),
 ]
 
 
 def geometry(out_dim, in_dim, rows):
     p = L.gemv_plan_info(out_dim, in_dim, rows)
     tr, nw, nj = p["tile_rows"], p["waves"], p["blocks_per_wave"]
-    g = dict(p, tr=tr, tl=tr.bit_length() - 1, qn=16 // tr, nw=nw, nj=nj, kw=32 * nj,
-             rs=32 * nj + 8, lpc=8 * nj, ni=2 * nj, kp=nw * 32 * nj, tiles=-(-out_dim // tr))
+    qn, rs, lpc = 16 // tr, 32 * nj + 8, 8 * nj
+    ncol = qn * rows
+    g = dict(p, tr=tr, tl=tr.bit_length() - 1, qn=qn, nw=nw, nj=nj, kw=32 * nj, rs=rs, lpc=lpc,
+             ni_all=2 * nj, ncol=ncol, ni=(ncol * lpc + 63) // 64,
+             reg=max(2 * ncol * rs, 608), kp=nw * 32 * nj, tiles=-(-out_dim // tr))
     return g
 
 
@@ -41,23 +46,26 @@ def geometry(out_dim, in_dim, rows):
 def test_launch_shape_fits(out_dim, in_dim, rows):
     g = geometry(out_dim, in_dim, rows)
     assert g["tr"] in (1, 2, 4, 8, 16) and g["tr"] >= rows
-    assert g["nj"] in (1, 2, 4) and 1 <= g["nw"] <= 16
+    assert g["nj"] in (1, 2, 4, 8) and 1 <= g["nw"] <= 16
     assert g["nw"] * 64 <= 1024
-    assert g["lds_bytes"] == g["nw"] * 64 * g["rs"] <= 160 * 1024
-    # the partial tile (64 lanes x 4 floats at word 4 l + 16 (l / 16): 304 words) fits the
-    # wave's region
-    assert 4 * (4 * 63 + 3 + 16 * 3 + 1) <= 64 * g["rs"]
+    # per wave: the hi and lo rows of the QN * rows columns (16-byte aligned), at least the
+    # partial tile (64 lanes x 4 floats at word 4 l + 16 (l / 16): 304 words)
+    assert g["reg"] % 8 == 0
+    assert 2 * (4 * 63 + 3 + 16 * 3 + 1) <= g["reg"]
+    assert g["lds_bytes"] == g["nw"] * g["reg"] * 2 <= 160 * 1024
     # the passes cover in_dim
     assert g["passes"] * g["qn"] * g["kp"] >= in_dim
     assert (g["passes"] - 1) * g["qn"] * g["kp"] < in_dim
-    # the dense x loads cover the 16 columns exactly
-    assert g["ni"] * 64 == 16 * g["lpc"]
+    # all the dense x loads cover the 16 slots exactly; those a launch makes hold every beam
+    assert g["ni_all"] * 64 == 16 * g["lpc"]
+    assert g["ncol"] <= 16 and g["ni"] <= g["ni_all"] and g["ni"] * 64 >= g["ncol"] * g["lpc"]
 
 
 @pytest.mark.parametrize("out_dim,in_dim,rows", SHAPES)
 def test_addresses_in_range_and_contraction_pairs_elements(out_dim, in_dim, rows):
     g = geometry(out_dim, in_dim, rows)
     tr, tl, qn, kw, rs, lpc, kp = g["tr"], g["tl"], g["qn"], g["kw"], g["rs"], g["lpc"], g["kp"]
+    ncol, reg = g["ncol"], g["reg"]
     lane = np.arange(64)
     m, grp = lane & 15, lane >> 4
     q, r = m >> tl, m & (tr - 1)
@@ -68,8 +76,8 @@ def test_addresses_in_range_and_contraction_pairs_elements(out_dim, in_dim, rows
     for ps in range(g["passes"]):
         for wave in range(g["nw"]):
             kb = ps * qn * kp + wave * kw
-            # dense x loads (slot v = beam v / QN over part v % QN, every slot loaded) and the
-            # LDS rows they fill: (column, element) -> (beam, x element)
+            # dense x loads (slot v = beam v / QN over part v % QN) and the LDS rows the slots of
+            # beams < rows fill: (LDS column, element) -> (beam, x element)
             written = {}
             for i in range(g["ni"]):
                 f = 64 * i + lane
@@ -81,16 +89,18 @@ def test_addresses_in_range_and_contraction_pairs_elements(out_dim, in_dim, rows
                 assert (b >= 0).all() and (k >= 0).all() and (k + 4 <= in_dim).all()
                 c4 = f % lpc
                 for L_ in range(64):
-                    n = (part[L_] << tl) + b_raw[L_]
-                    assert n < 16 and 4 * c4[L_] + 4 <= kw and (16 + n) * rs + 4 * c4[L_] + 4 <= 32 * rs
+                    if b_raw[L_] >= rows:  # a slot past the beams: loaded, not kept
+                        continue
+                    n = part[L_] * rows + b_raw[L_]
+                    assert n < ncol and 4 * c4[L_] + 4 <= kw
+                    assert (ncol + n) * rs + 4 * c4[L_] + 4 <= reg and n * rs + kw < reg
                     for e in range(4):
                         key = (n, 4 * c4[L_] + e)
                         assert key not in written
                         written[key] = (b_raw[L_], kb + part[L_] * kp + 4 * c4[L_] + e)
-            # every valid column is fully written
-            for n in range(16):
-                if (n & (tr - 1)) < rows:
-                    assert all((n, off) in written for off in range(kw))
+            # every column is fully written
+            for n in range(ncol):
+                assert all((n, off) in written for off in range(kw))
             for j in range(g["nj"]):
                 kw_ = kb + q * kp + 32 * j + 8 * grp
                 kc = np.minimum(kw_, in_dim - 8)
@@ -103,8 +113,9 @@ def test_addresses_in_range_and_contraction_pairs_elements(out_dim, in_dim, rows
                             seen[k] += 1
                         if (n_col & (tr - 1)) < rows:
                             off = 32 * j + 8 * grp[L_] + e
-                            assert off < kw and n_col * rs + off < (n_col + 1) * rs
-                            bb, kx = written[(n_col, off)]
+                            ncm = (n_col >> tl) * rows + (n_col & (tr - 1))
+                            assert off < kw and (ncol + ncm) * rs + off < reg
+                            bb, kx = written[(ncm, off)]
                             # B column n = q' TR + b holds beam b over part q' = n >> tl, at the
                             # element the A rows of the same part contract with
                             assert bb == (n_col & (tr - 1))

@@ -72,6 +72,25 @@ def test_vocab_logits_blocks_and_ragged_steps(gpu, d, rows, vocab, blk):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("offset,pitch", [(1, 1025), (4, 1032), (0, 1028)])
+def test_vocab_logits_strided_activations(gpu, offset, pitch):
+    """Activation rows read through a row stride wider than d, starting off a 16-byte boundary
+    (the element-wise quantization loop) or on one (the register path): logits equal the
+    oracle's bit for bit."""
+    d, rows, vocab = 1024, 5, 3001
+    rng = np.random.default_rng(79 + offset + pitch)
+    emb = (rng.standard_normal((vocab, d)) / np.sqrt(d)).astype(np.float32)
+    full = rng.standard_normal((rows, pitch)).astype(np.float32)
+    x = full[:, offset:offset + d]
+    iv = Int8Vocab(torch.from_numpy(emb).to(gpu))
+    xg = torch.from_numpy(full).to(gpu)[:, offset:offset + d]
+    assert xg.stride(0) == pitch
+    got = iv(xg).cpu().numpy()
+    q, sc, corr = og.vocab_quantize(emb, 32)
+    want = og.vocab_logits(q, sc, corr, np.ascontiguousarray(x), 32)
+    np.testing.assert_array_equal(got, want)
+
+
 @pytest.mark.parametrize("out_dim,in_dim,rows", [(1536, 384, 1), (1024, 1024, 5),
                                                  (4096, 1024, 5), (1024, 4096, 9), (1023, 1280, 16),
                                                  (3840, 1280, 5)])
@@ -162,7 +181,9 @@ SPECIALIZED = [(1024, 1024, 5), (1024, 1024, 6), (1024, 1024, 7), (1024, 1024, 8
                (4096, 1024, 1), (3072, 1024, 4), (4096, 1024, 5), (3072, 1024, 8),
                (4096, 1024, 9), (4096, 1024, 16), (1024, 4096, 5), (1024, 4096, 6),
                (1024, 4096, 8), (1024, 1024, 1), (1024, 4096, 1), (1280, 1280, 5),
-               (1280, 1280, 6), (3840, 1280, 5), (5120, 1280, 6), (1280, 5120, 5)]
+               (1280, 1280, 6), (3840, 1280, 5), (5120, 1280, 5), (5120, 1280, 6),
+               (1280, 5120, 5), (1280, 5120, 4), (1280, 5120, 6), (1280, 6144, 5),
+               (1024, 20000, 9)]
 
 
 @pytest.mark.parametrize("out_dim,in_dim,rows", SPECIALIZED)
