@@ -130,11 +130,11 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int ps = 0; ps < (SPEC ? 1 : p.passes); ++ps) {
     const int kb = ps * qn * kp + wave * KW;
-    // Dense x: load slot v = 0..15 is beam v / QN over part v % QN (column n = part TR + beam),
+    // Dense x: load slot v = 0..15 is beam v / QN over part v % QN (MFMA column part TR + beam),
     // LPC lanes per slot, 4 elements each. Slots of beams >= rows load a valid beam's elements
     // and fill LDS rows that are never read; no branch, no division.
-    // (A generic instance with more than 8 loads takes the rest after the weights: all of them
-    // beside the weights would exceed the 128 registers of a 1024-lane workgroup.)
+    // (A generic instance with more than 8 loads issues 4 before the weights and each later one
+    // 4 slots ahead of its use, so that 4 stay in flight without holding all 16 in registers.)
     constexpr int NX1 = (SPEC || NI <= 8) ? NI : 4;
     f32x4 xv[NI];
     auto load_x = [&](int i) __attribute__((always_inline)) {
@@ -156,11 +156,15 @@ __global__ __launch_bounds__(1024) void gemv_f16_kernel(GemvParams p, QkvCachePa
     // split the loaded slots that hold a beam (the first QN * rows; the rest are never read)
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
+      // every address is clamped inside x: the prefetch needs no test of ni (a load under a
+      // branch would make the compiler wait for every load at the join)
+      if constexpr (NX1 < NI) {
+        if (i + NX1 < NI) load_x(i + NX1);
+      }
       if (SPEC ? i >= NXL : i >= ni) {  // wave-uniform
         if constexpr (NX1 < NI) continue;  // (a loop of 16 with a load would not unroll on break)
         else break;
       }
-      if (i >= NX1) load_x(i);
       const int f = 64 * i + lane, v = f / LPC, c4 = f % LPC;
       const int b = v >> (4 - tl), part = v & (qn - 1);
       const bool ok = kb + part * kp + 4 * c4 < p.in_dim;
