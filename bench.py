@@ -54,7 +54,8 @@ def parse():
                             "stamps,keys",
                     help="comma list of extra legs beside the headline encoder run: decode, "
                          "decode_ref, state, block, gemv, tiny, small, prefill, floor, pipes, "
-                         "stamps, keys, or 'none'; "
+                         "stamps, keys, or 'none'; gemv_large (not run by default): the "
+                         "decoder GEMVs at whisper-large width; "
                          "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
@@ -1021,8 +1022,9 @@ def gemv_bench(torch, steps, warmup, beams=5, n=1024, layers=24, vocab=51865):
     torch.cuda.synchronize()
     us_vocab = e0.elapsed_time(e1) * 1e3 / (steps * per_graph)
     del vgraph, ivs
-    # per shape: graphs of 24 dependent launches over distinct weights, two sets alternating so
-    # that the weights replayed (2 x 24 matrices) exceed the 256 MB MALL for the larger shapes
+    # per shape: graphs of `layers` dependent launches over distinct weights, two sets
+    # alternating so that the weights replayed (2 x layers matrices) exceed the 256 MB MALL for
+    # the larger shapes
     per_launch = {}
     for o, i in dict.fromkeys(shapes):  # the distinct shapes, in order
         si = shapes.index((o, i))
@@ -1276,6 +1278,13 @@ def main():
             f"projection {gv['vocab_us']:.1f} us ({gv['vocab_gbps']:.0f} GB/s); per launch "
             + ", ".join(f"{k} {v:.2f} us" for k, v in gv["us_per_launch"].items()))
         extras["decoder_gemv_beam5"] = gv
+    if "gemv_large" in legs:
+        log("decoder GEMVs: beam-5 whisper-large step (d 1280, 32 layers) ...")
+        gl = gemv_bench(torch, 50, 5, n=1280, layers=32, vocab=51866)
+        log(f"decoder GEMVs large: {gl['us_per_step']:.1f} us/step ({gl['gbps']:.0f} GB/s); "
+            f"vocabulary projection {gl['vocab_us']:.1f} us; per launch "
+            + ", ".join(f"{k} {v:.2f} us" for k, v in gl["us_per_launch"].items()))
+        extras["decoder_gemv_large_beam5"] = gl
     if "tiny" in legs:
         log("encoder: whisper-tiny f32 ...")
         tiny = encoder_bench(torch, fa, max(args.steps * 5, 50), args.warmup, 4, B=1, H=6,
