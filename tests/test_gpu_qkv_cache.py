@@ -44,11 +44,13 @@ def _weights(rng, n, in_dim, device):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("rows,with_bias", [(5, True), (5, False), (1, True)])
-def test_fused_step_equals_gemv_bias_append(gpu, dtype, rows, with_bias):
-    """whisper-medium widths (16 heads x 64, in 1024), ragged lengths: q, the K/V caches and the
-    lengths after advance + fused call equal GEMV + bias + append bit for bit."""
-    rng = np.random.default_rng(90 + rows)
-    heads, d, cap, in_dim = 16, 64, 80, 1024
+@pytest.mark.parametrize("heads,in_dim", [(16, 1024), (20, 1280)])
+def test_fused_step_equals_gemv_bias_append(gpu, dtype, rows, with_bias, heads, in_dim):
+    """whisper-medium (16 heads x 64, in 1024) and whisper-large (20 x 64, in 1280) widths,
+    ragged lengths: q, the K/V caches and the lengths after advance + fused call equal GEMV +
+    bias + append bit for bit."""
+    rng = np.random.default_rng(90 + rows + heads)
+    d, cap = 64, 80
     n = heads * d
     lens = [0, 3, 40, 78, 79][:rows]
     gm = _weights(rng, n, in_dim, gpu)
