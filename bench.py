@@ -50,12 +50,12 @@ def parse():
                     help="decode leg without HIP graphs (for counter collection)")
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--legs",
-                    default="decode,decode_ref,state,block,gemv,tiny,small,prefill,floor,pipes,"
-                            "stamps,keys",
+                    default="decode,decode_ref,state,block,gemv,gemv_large,tiny,small,prefill,"
+                            "floor,pipes,stamps,keys",
                     help="comma list of extra legs beside the headline encoder run: decode, "
-                         "decode_ref, state, block, gemv, tiny, small, prefill, floor, pipes, "
-                         "stamps, keys, or 'none'; gemv_large (not run by default): the "
-                         "decoder GEMVs at whisper-large width; "
+                         "decode_ref, state, block, gemv, gemv_large (the decoder GEMVs at "
+                         "whisper-large width), tiny, small, prefill, floor, pipes, stamps, keys, "
+                         "or 'none'; "
                          "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
