@@ -55,7 +55,8 @@ def parse():
                     help="comma list of extra legs beside the headline encoder run: decode, "
                          "decode_ref, state, block, gemv, gemv_large (the decoder GEMVs at "
                          "whisper-large width), tiny, small, prefill, floor, pipes, stamps, keys, "
-                         "or 'none'; "
+                         "or 'none'; 'gemv_probe' alone runs only a few decoder GEMV calls "
+                         "for counter collection; "
                          "'copy' alone "
                          "runs only the copy calibration used to scale HBM byte counters")
     return ap.parse_args()
@@ -153,6 +154,32 @@ def copy_bench(torch, steps, nbytes=1 << 30):
     ms = e0.elapsed_time(e1) / steps
     return {"bytes_each_way": nbytes, "us_per_copy": ms * 1e3,
             "gbps": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
+def gemv_probe(torch, calls=3, beams=5, n=1024, vocab=51865):
+    """The whisper-medium decoder's GEMV shapes at `beams` beams and its int8 vocabulary
+    projection, `calls` eager calls each with fresh weights per shape, untimed: a short program
+    for rocprofv3 --pmc (the gemv leg's graphs are too many dispatches for counter collection).
+    Returns the algorithmic bytes per call of each shape."""
+    from ffai_amd.gemv import F16Gemv, Int8Vocab
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(9)
+    out = {}
+    for o, i in ((3 * n, n), (n, n), (4 * n, n), (n, 4 * n)):
+        m = F16Gemv(torch.randn(o, i, generator=g, device=dev) / i ** 0.5)
+        x = torch.randn(beams, i, generator=g, device=dev)
+        for _ in range(calls):
+            m(x)
+        out[f"{o}x{i}"] = o * i * 2 + beams * (i + o) * 4
+    iv = Int8Vocab(torch.randn(vocab, n, generator=g, device=dev) / n ** 0.5)
+    ws = torch.empty(iv.workspace_bytes(beams), dtype=torch.uint8, device=dev)
+    x = torch.randn(beams, n, generator=g, device=dev)
+    for _ in range(calls):
+        iv(x, workspace=ws)
+    torch.cuda.synchronize()
+    out[f"vocab {vocab}x{n}"] = vocab * n + vocab * (n // 32) * 4 + vocab * 4 + beams * (n + vocab) * 4
+    return {"calls": calls, "beams": beams, "algorithmic_bytes_per_call": out}
 
 
 # ------------------------------------------------------------------------------------------
@@ -1236,6 +1263,9 @@ def main():
     legs = set() if args.skip_extras else {x for x in args.legs.split(",") if x and x != "none"}
     if legs == {"copy"}:
         print(json.dumps({"copy_calibration": copy_bench(torch, max(args.steps, 1))}), flush=True)
+        return
+    if legs == {"gemv_probe"}:
+        print(json.dumps({"gemv_probe": gemv_probe(torch)}), flush=True)
         return
     log("encoder: whisper-large-v3 bf16 ...")
     enc = encoder_bench(torch, fa, args.steps, args.warmup, args.layers)
